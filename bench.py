@@ -1,0 +1,285 @@
+"""Bench for the MI355X puter backend.  Prints ONE JSON line.
+
+Primary metric: the bf16 RMSNorm / LayerNorm
+bandwidth sweep fused with the gated-residual add, rows in {1024, 16384, 65536}
+x hidden in {2048, 4096, 8192}.  One "step" = one pass over the 9 shapes, each
+running the fused GatedResidual+RMSNorm and GatedResidual+LayerNorm once
+(18 launches).  value = algorithmic bytes of the step (8 B/elem: read residual
+and branch, write hidden and normed) / the step's GPU time, inputs resident in
+HBM.  The other configs' figures are reported under "configs".
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only norm,rope,...]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+ROWS = (1024, 16384, 65536)
+HIDDEN = (2048, 4096, 8192)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on the stream the kernels are launched on (torch's current)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, iters):
+        t = self.torch
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        t.cuda.synchronize()
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / iters  # ms
+
+
+def norm_sweep(torch, be, puter, steps, warmup):
+    """returns (metric dict, dominant-kernel roofline dict)."""
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
+    rmax, hmax = max(ROWS), max(HIDDEN)
+    n = rmax * hmax
+    bf = torch.bfloat16
+    res = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+    br = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+    hid = torch.empty(n, device="cuda", dtype=bf)
+    out = torch.empty(n, device="cuda", dtype=bf)
+    mod = torch.randn(3 * hmax, device="cuda", dtype=bf, generator=gen)
+    gamma = 1 + 0.02 * torch.randn(hmax, device="cuda", dtype=torch.float32, generator=gen)
+    gamma = gamma.to(bf)
+    beta = (0.02 * torch.randn(hmax, device="cuda", dtype=torch.float32, generator=gen)).to(bf)
+    cfg = puter.RMSNormConfig(1e-5)
+    launches = []
+    for r in ROWS:
+        for h in HIDDEN:
+            def rms(r=r, h=h):
+                be.GatedResidualRMSNorm(cfg, res, br, mod, gamma, hid, out, r, h, r, 3 * h, 0, puter.BF16)
+
+            def ln(r=r, h=h):
+                be.GatedResidualLayerNorm(res, br, mod, gamma, beta, hid, out, r, h, r, 3 * h, 0, puter.BF16)
+            launches.append((r, h, "rms", rms))
+            launches.append((r, h, "ln", ln))
+    step_bytes = sum(8 * r * h for r, h, _, _ in launches)
+
+    def step():
+        for _, _, _, fn in launches:
+            fn()
+
+    timer = Timer(torch)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ms = timer.time(step, steps)
+    # per-shape figures and the dominant kernel, timed live with events
+    per = {}
+    for r, h, kind, fn in launches:
+        fn()
+        t = timer.time(fn, 20)
+        per[f"{kind}_{r}x{h}"] = round(8 * r * h / (t * 1e-3) / 1e9, 1)
+    dom = [x for x in launches if x[0] == rmax and x[1] == hmax and x[2] == "rms"][0]
+    dom_ms = timer.time(dom[3], 50)
+    dom_bytes = 8 * rmax * hmax
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "norm_wave_kernel<bf16,RMS,GR,16> (fused gated residual + RMSNorm)",
+            "workload": f"{rmax}x{hmax} bf16, {dom_bytes} B/launch", "avg_launch_us": round(dom_ms * 1e3, 2)}
+    del res, br, hid, out
+    torch.cuda.empty_cache()
+    return ms, step_bytes, per, roof
+
+
+def rope_swiglu_casts(torch, be, puter):
+    """RoPE on Q [8192,32,128] + K [8192,8,128] (theta 5e5), SwiGLU
+    over [8192,14336], bf16/f16/fp8 <-> f32 casts over the same tensors."""
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0002)
+    bf = torch.bfloat16
+    S = 8192
+    q = torch.randn(S * 32 * 128, device="cuda", dtype=bf, generator=gen)
+    k = torch.randn(S * 8 * 128, device="cuda", dtype=bf, generator=gen)
+    gate = torch.randn(S * 14336, device="cuda", dtype=bf, generator=gen)
+    up = torch.randn(S * 14336, device="cuda", dtype=bf, generator=gen)
+    act = torch.empty_like(gate)
+    cfg = puter.RoPEConfig(BaseFreq=500000.0)
+    timer = Timer(torch)
+    res = {}
+
+    def rope():
+        be.RoPE(cfg, q, q, S, 32, 128, puter.BF16)
+        be.RoPE(cfg, k, k, S, 8, 128, puter.BF16)
+    rope()
+    t = timer.time(rope, 20)
+    res["rope_qk_bf16_GBs"] = round(4 * (q.numel() + k.numel()) / (t * 1e-3) / 1e9, 1)
+
+    def swiglu():
+        be.SwiGLUTensors(act, gate, up, gate.numel(), puter.BF16)
+    swiglu()
+    t = timer.time(swiglu, 20)
+    res["swiglu_bf16_GBs"] = round(6 * gate.numel() / (t * 1e-3) / 1e9, 1)
+    f32 = torch.empty(gate.numel(), device="cuda", dtype=torch.float32)
+    narrow = torch.empty(gate.numel(), device="cuda", dtype=torch.int16)
+    n8 = torch.empty(gate.numel(), device="cuda", dtype=torch.uint8)
+    for name, fmt, buf, eb in (("bf16", puter.BF16, narrow, 2), ("f16", puter.F16, narrow, 2),
+                               ("fp8e4m3", puter.F8E4M3, n8, 1)):
+        be.Cast(f32, puter.F32, gate, puter.BF16, gate.numel())
+        t1 = timer.time(lambda: be.Cast(buf, fmt, f32, puter.F32, gate.numel()), 10)
+        t2 = timer.time(lambda: be.Cast(f32, puter.F32, buf, fmt, gate.numel()), 10)
+        res[f"cast_f32_to_{name}_GBs"] = round((4 + eb) * gate.numel() / (t1 * 1e-3) / 1e9, 1)
+        res[f"cast_{name}_to_f32_GBs"] = round((4 + eb) * gate.numel() / (t2 * 1e-3) / 1e9, 1)
+    del q, k, gate, up, act, f32, narrow, n8
+    torch.cuda.empty_cache()
+    return res
+
+
+def prefill(torch, be, puter):
+    """causal GQA prefill bf16, B4 S4096 Hq32 Hkv8 D128."""
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0003)
+    B, S, H, KV, D = 4, 4096, 32, 8, 128
+    sc = 1.0 / math.sqrt(D)
+    q = (torch.randn(B * S * H * D, device="cuda", generator=gen) * sc).to(torch.bfloat16)
+    k = (torch.randn(B * S * KV * D, device="cuda", generator=gen) * sc).to(torch.bfloat16)
+    v = (torch.randn(B * S * KV * D, device="cuda", generator=gen) * sc).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    cfg = puter.MultiHeadAttentionConfig(H, D, True, 0, 0.0, KV)
+    fn = lambda: be.MultiHeadAttentionBatched(cfg, q, k, v, o, B, S, S, puter.BF16)  # noqa: E731
+    fn()
+    t = Timer(torch).time(fn, 5)
+    flops = 4.0 * B * H * D * S * (S + 1) / 2
+    tf = flops / (t * 1e-3) / 1e12
+    return {"prefill_ms": round(t, 3), "prefill_TFLOPs": round(tf, 1),
+            "prefill_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
+def decode(torch, be, puter, fp8):
+    """paged decode, B64, ctx ~ U[512, 8192], page 16, Hq32 Hkv8 D128."""
+    import numpy as np
+    rng = np.random.default_rng(0x5EED0004)
+    B, H, KV, D, PS = 64, 32, 8, 128, 16
+    ctx = rng.integers(512, 8193, B).astype(np.int32)
+    npages = (ctx + PS - 1) // PS
+    total = int(npages.sum())
+    perm = rng.permutation(total).astype(np.int32)
+    maxp = int(npages.max())
+    table = np.zeros((B, maxp), np.int32)
+    at = 0
+    for i in range(B):
+        table[i, :npages[i]] = perm[at:at + npages[i]]
+        at += npages[i]
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0005)
+    q = torch.randn(B * H * D, device="cuda", generator=gen).to(torch.bfloat16)
+    n = total * PS * KV * D
+    if fp8:
+        kp = (torch.randn(n, device="cuda", generator=gen) * 64).to(torch.float8_e4m3fn)
+        vp = (torch.randn(n, device="cuda", generator=gen) * 64).to(torch.float8_e4m3fn)
+        ks = torch.full((KV,), 1 / 64, device="cuda")
+        vs = torch.full((KV,), 1 / 64, device="cuda")
+        fmt, eb = puter.F8E4M3, 1
+    else:
+        kp = torch.randn(n, device="cuda", generator=gen).to(torch.bfloat16)
+        vp = torch.randn(n, device="cuda", generator=gen).to(torch.bfloat16)
+        ks = vs = None
+        fmt, eb = puter.BF16, 2
+    maxc = int(ctx.max())
+    wsb = be.PagedDecodeWorkspaceBytes(B, H, D, maxc)
+    ws = torch.empty(wsb, device="cuda", dtype=torch.uint8)
+    out = torch.empty_like(q)
+    tt = torch.from_numpy(table).cuda()
+    cc = torch.from_numpy(ctx).cuda()
+    fn = lambda: be.PagedDecodeAttention(q, kp, vp, tt, cc, B, maxp, PS, total, H, KV, D, maxc, ks, vs, fmt,  # noqa: E731
+                                         out, ws, wsb)
+    fn()
+    t = Timer(torch).time(fn, 20)
+    kv_bytes = int(ctx.sum()) * KV * D * 2 * eb
+    name = "fp8" if fp8 else "bf16"
+    return {f"decode_{name}_us": round(t * 1e3, 1),
+            f"decode_{name}_GBs": round(kv_bytes / (t * 1e-3) / 1e9, 1),
+            f"decode_{name}_hbm_frac": round(kv_bytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "decode_sum_ctx": int(ctx.sum())}
+
+
+def cpu_baseline():
+    """The oracle's fused GatedResidual+RMSNorm (bf16) on a bounded sample of
+    the primary workload, threaded over rows on all host cores."""
+    import numpy as np
+    import oracle as O
+    cores = os.cpu_count() or 1
+    O.set_threads(cores)
+    rows, h = 2048, 8192
+    res = O.from_f32(O.normal(11, rows * h).reshape(rows, h), O.BF16)
+    br = O.from_f32(O.normal(12, rows * h).reshape(rows, h), O.BF16)
+    mod = O.from_f32(O.normal(13, 3 * h).reshape(1, 3 * h), O.BF16)
+    g = O.from_f32(O.normal(14, h, 1.0, 0.02), O.BF16)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        hid = O.gated_residual(res, br, mod, rows, 0, O.BF16)
+        O.rmsnorm(hid, g, 1e-5, O.BF16)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 200:
+            break
+    gbs = 8 * rows * h * reps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle fused GatedResidual+RMSNorm bf16, {rows}x{h}, {reps} reps in {el:.1f}s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default="norm,rope,prefill,decode,cpu")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "every kernel shards by rows/sequences with no exchange", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import puter_amd as puter
+    be = puter.Backend()
+    only = set(args.only.split(","))
+    ms, step_bytes, per, roof = norm_sweep(torch, be, puter, args.steps, args.warmup)
+    log(f"norm sweep: {ms:.3f} ms/step, {step_bytes / (ms * 1e-3) / 1e9:.1f} GB/s")
+    configs = {"norm_sweep_GBs": per}
+    if "rope" in only:
+        configs.update(rope_swiglu_casts(torch, be, puter))
+        log(f"rope/swiglu/casts: {configs}")
+    if "prefill" in only:
+        configs.update(prefill(torch, be, puter))
+        log(f"prefill: {configs.get('prefill_TFLOPs')} TFLOP/s")
+    if "decode" in only:
+        configs.update(decode(torch, be, puter, False))
+        configs.update(decode(torch, be, puter, True))
+        log("decode done")
+    cpu = cpu_baseline() if "cpu" in only else None
+    value = step_bytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "HBM GB/s for norm/RoPE/act; attention TFLOP/s; % of MI355X roofline",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "fused GatedResidual+RMSNorm/LayerNorm bf16 sweep, rows {1024,16384,65536} "
+                               "x hidden {2048,4096,8192}, eps 1e-5 (BASELINE configs[1])",
+                   "bytes_per_step": step_bytes, "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,139 @@
+// MultiHeadAttention (GQA, causal, sliding window, ALiBi) for any dtype.
+// Reference: device/cpu/attention/compute.go:31-90 and typed_compute.go:10-237:
+// kv head = h / (H / Hkv); scale = float32(1/sqrt(float64(D))); score = dot * scale
+// (16-bit dots rounded to the 16-bit format); causal mask k > q + seqK - seqQ;
+// window mask q - k >= WindowSize; ALiBi score += slope * (k - q); softmax;
+// out[d] = sum_k p_k v[k, d]; an all-masked row yields zeros (softmax.go:33-75).
+//
+// This file holds the general kernel (one block per (batch, head, query row),
+// online softmax over 256-key chunks staged in LDS, f32 accumulation) and the
+// dispatch: bf16 causal/non-causal prefill with D in {64, 128} and no
+// window/ALiBi goes to the MFMA flash kernel (prefill.hip).
+#include "common.hpp"
+
+namespace puter {
+
+struct MhaArgs {
+    const void *q, *k, *v;
+    void *o;
+    int64_t batch, seq_q, seq_k, heads, kv_heads, dim;
+    int causal;
+    int64_t window;
+    float alibi;
+    float scale;
+};
+
+// Defined in prefill.hip: returns true if it launched.
+bool launch_prefill_mfma(const MhaArgs &a, int dtype, hipStream_t s, int *status);
+
+template <int DT>
+__global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {
+    using T = typename Elem<DT>::T;
+    __shared__ float qrow[256];
+    __shared__ float pk[256];
+    __shared__ float red[4];
+    const int64_t qi = blockIdx.x;
+    const int64_t h = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int64_t D = a.dim;
+    const int64_t group = a.heads / a.kv_heads;
+    const int64_t kvh = h / group;
+    const int64_t qs = a.heads * D, ks = a.kv_heads * D;
+    const T *Q = reinterpret_cast<const T *>(a.q) + (b * a.seq_q + qi) * qs + h * D;
+    const T *K = reinterpret_cast<const T *>(a.k) + b * a.seq_k * ks + kvh * D;
+    const T *V = reinterpret_cast<const T *>(a.v) + b * a.seq_k * ks + kvh * D;
+    T *O = reinterpret_cast<T *>(a.o) + (b * a.seq_q + qi) * qs + h * D;
+    for (int64_t d = tid; d < D; d += 256) qrow[d] = Elem<DT>::load(Q[d]);
+    __syncthreads();
+    // keys visible to this row form [k_lo, k_hi)
+    int64_t k_hi = a.seq_k;
+    if (a.causal) k_hi = min(k_hi, qi + a.seq_k - a.seq_q + 1);
+    int64_t k_lo = 0;
+    if (a.window > 0) k_lo = max(k_lo, qi - a.window + 1);
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    const int wave = tid >> 6, lane = tid & 63;
+    for (int64_t c0 = k_lo; c0 < k_hi; c0 += 256) {
+        const int64_t k = c0 + tid;
+        float s = -INFINITY;
+        if (k < k_hi) {
+            const T *kr = K + k * ks;
+            float dot = 0.0f;
+            for (int64_t d = 0; d < D; ++d) dot += qrow[d] * Elem<DT>::load(kr[d]);
+            s = round_reduction<DT>(dot) * a.scale;
+            if (a.alibi != 0.0f) s += a.alibi * (float)(k - qi);
+        }
+        float cm = wave_max(s);
+        __syncthreads();
+        if (lane == 0) red[wave] = cm;
+        __syncthreads();
+        cm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float m_new = fmaxf(m, cm);
+        const float p = (s == -INFINITY) ? 0.0f : expf(s - m_new);
+        pk[tid] = p;
+        float ps = wave_sum(p);
+        __syncthreads();
+        if (lane == 0) red[wave] = ps;
+        __syncthreads();
+        ps = red[0] + red[1] + red[2] + red[3];
+        const float alpha = (m == -INFINITY) ? 0.0f : expf(m - m_new);
+        l = l * alpha + ps;
+        if (tid < D) {
+            float part = 0.0f;
+            const int64_t n = min((int64_t)256, k_hi - c0);
+            for (int64_t j = 0; j < n; ++j) part += pk[j] * Elem<DT>::load(V[(c0 + j) * ks + tid]);
+            acc = acc * alpha + part;
+        }
+        m = m_new;
+        __syncthreads();
+    }
+    if (tid < D) O[tid] = Elem<DT>::store(l > 0.0f ? acc / l : 0.0f);
+}
+
+static int run_mha(const puter_mha_config *config, const void *q, const void *k, const void *v,
+                   void *o, int64_t batch, int64_t seq_q, int64_t seq_k, int dtype, hipStream_t s) {
+    if (!config) return fail(PUTER_ERR_NIL, "mha: nil config");
+    if (!is_norm_dtype(dtype)) return fail(PUTER_ERR_INVALID, "mha: unsupported dtype %d", dtype);
+    if (batch < 0 || seq_q < 0 || seq_k < 0) return fail(PUTER_ERR_INVALID, "mha: negative shape");
+    const int64_t H = config->num_heads, D = config->head_dim;
+    const int64_t kvh = config->kv_head_count > 0 ? config->kv_head_count : H;
+    if (H <= 0 || D <= 0) return fail(PUTER_ERR_INVALID, "mha: heads and head_dim must be positive");
+    if (H % kvh != 0) return fail(PUTER_ERR_INVALID, "mha: %lld heads not divisible by %lld kv heads",
+                                  (long long)H, (long long)kvh);
+    if (D > 256) return fail(PUTER_ERR_INVALID, "mha: head_dim %lld > 256 unsupported", (long long)D);
+    if (batch == 0 || seq_q == 0 || seq_k == 0) return PUTER_OK;
+    if (!q || !k || !v || !o) return fail(PUTER_ERR_NIL, "mha: nil buffer");
+    if (seq_q > 0x7FFFFFFF || H > 65535 || batch > 65535) return fail(PUTER_ERR_INVALID, "mha: grid too large");
+    MhaArgs a{q, k, v, o, batch, seq_q, seq_k, H, kvh, D, config->causal ? 1 : 0,
+              config->window_size, config->alibi_slope, (float)(1.0 / sqrt((double)D))};
+    int status = PUTER_OK;
+    if (launch_prefill_mfma(a, dtype, s, &status)) return status;
+    const dim3 grid((unsigned)seq_q, (unsigned)H, (unsigned)batch);
+    switch (dtype) {
+    case PUTER_F32: mha_generic_kernel<PUTER_F32><<<grid, 256, 0, s>>>(a); break;
+    case PUTER_BF16: mha_generic_kernel<PUTER_BF16><<<grid, 256, 0, s>>>(a); break;
+    case PUTER_F16: mha_generic_kernel<PUTER_F16><<<grid, 256, 0, s>>>(a); break;
+    }
+    return check_launch("mha");
+}
+
+}  // namespace puter
+
+using namespace puter;
+
+extern "C" {
+
+int puter_hip_multi_head_attention(const puter_mha_config *config, const void *query,
+                                   const void *key, const void *value, void *output,
+                                   int64_t seq_q, int64_t seq_k, int dtype, void *stream) {
+    return run_mha(config, query, key, value, output, 1, seq_q, seq_k, dtype, as_stream(stream));
+}
+
+int puter_hip_multi_head_attention_batched(const puter_mha_config *config, const void *query,
+                                           const void *key, const void *value, void *output,
+                                           int64_t batch, int64_t seq_q, int64_t seq_k,
+                                           int dtype, void *stream) {
+    return run_mha(config, query, key, value, output, batch, seq_q, seq_k, dtype, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+// Paged KV cache: KVPageWrite / KVPageGather device hooks.
+// Reference: execution/page_intrinsic.go:13-24 (hook signatures), :135-352
+// (callers), CPU semantics device/cpu/shape/page_generic.go:5-95 (row copies of
+// `inner` elements) and the bounds rules of device/cpu/shape/page.go:139-146,191-203.
+//
+// Pure byte movement: rows are copied with 16-byte vectors when the row size and
+// the pointers allow it, one 64-lane wave per row (a 2 KiB bf16 row of 8 heads x
+// 128 is two wave-wide loads).  Page ids are checked on the device: a row whose
+// id or slot is out of range is skipped (write) or zero-filled (gather), so no
+// access ever leaves the storage; the host cannot read the device page table
+// without a synchronisation the reference's zero-host-sync contract forbids.
+#include "common.hpp"
+
+namespace puter {
+
+template <typename V>
+__global__ __launch_bounds__(256) void page_gather_kernel(const char *__restrict__ storage,
+                                                          const int32_t *__restrict__ table,
+                                                          char *__restrict__ out, int64_t page_count,
+                                                          int64_t page_size, int64_t row_units,
+                                                          int64_t out_rows) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= out_rows) return;
+    const int32_t id = table[row / page_size];
+    V *dst = reinterpret_cast<V *>(out) + row * row_units;
+    if (id < 0 || id >= page_count) {
+        for (int64_t u = lane; u < row_units; u += 64) dst[u] = V{};
+        return;
+    }
+    const V *src = reinterpret_cast<const V *>(storage) + ((int64_t)id * page_size + row % page_size) * row_units;
+    for (int64_t u = lane; u < row_units; u += 64) dst[u] = src[u];
+}
+
+template <typename V>
+__global__ __launch_bounds__(256) void page_write_kernel(char *__restrict__ storage,
+                                                         const char *__restrict__ values,
+                                                         const int32_t *__restrict__ ids,
+                                                         const int32_t *__restrict__ offsets,
+                                                         int64_t page_count, int64_t page_size,
+                                                         int64_t row_units, int64_t value_rows) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= value_rows) return;
+    const int32_t id = ids[row], off = offsets[row];
+    if (id < 0 || id >= page_count || off < 0 || off >= page_size) return;
+    V *dst = reinterpret_cast<V *>(storage) + ((int64_t)id * page_size + off) * row_units;
+    const V *src = reinterpret_cast<const V *>(values) + row * row_units;
+    for (int64_t u = lane; u < row_units; u += 64) dst[u] = src[u];
+}
+
+static bool all_aligned(const void *const *p, int n, uintptr_t mask) {
+    for (int i = 0; i < n; ++i)
+        if (reinterpret_cast<uintptr_t>(p[i]) & mask) return false;
+    return true;
+}
+
+}  // namespace puter
+
+using namespace puter;
+
+extern "C" {
+
+int puter_hip_kv_page_write(const void *storage, const void *values, const int32_t *page_ids,
+                            const int32_t *offsets, void *output, int64_t page_count,
+                            int64_t page_size, int64_t inner, int64_t value_rows,
+                            int64_t storage_offset, int dtype, void *stream) {
+    const int es = dtype_bytes(dtype);
+    if (es == 0) return fail(PUTER_ERR_INVALID, "kv page write: unsupported dtype %d", dtype);
+    if (page_count < 0 || page_size <= 0 || inner < 0 || value_rows < 0 || storage_offset < 0)
+        return fail(PUTER_ERR_INVALID, "kv page write: invalid shape");
+    if (value_rows == 0 || inner == 0) return PUTER_OK;
+    if (!storage || !values || !page_ids || !offsets || !output) return fail(PUTER_ERR_NIL, "kv page write: nil buffer");
+    hipStream_t s = as_stream(stream);
+    const size_t row_bytes = (size_t)inner * es;
+    const char *src_base = static_cast<const char *>(storage) + (size_t)storage_offset * es;
+    char *dst_base = static_cast<char *>(output) + (size_t)storage_offset * es;
+    // pageWrite*Generic copies storage to output first (page_generic.go:23); the
+    // device caller passes output == storage (page_intrinsic.go:199-205), a no-op
+    if (dst_base != src_base) {
+        hipError_t e = hipMemcpyAsync(dst_base, src_base, (size_t)(page_count * page_size) * row_bytes,
+                                      hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return fail(PUTER_ERR_LAUNCH, "kv page write: copy: %s", hipGetErrorString(e));
+    }
+    const unsigned blocks = (unsigned)((value_rows + 3) / 4);
+    const void *ptrs[2] = {dst_base, values};
+    if (row_bytes % 16 == 0 && all_aligned(ptrs, 2, 15))
+        page_write_kernel<uint4><<<blocks, 256, 0, s>>>(dst_base, (const char *)values, page_ids, offsets,
+                                                        page_count, page_size, (int64_t)(row_bytes / 16), value_rows);
+    else if (row_bytes % 4 == 0 && all_aligned(ptrs, 2, 3))
+        page_write_kernel<uint32_t><<<blocks, 256, 0, s>>>(dst_base, (const char *)values, page_ids, offsets,
+                                                           page_count, page_size, (int64_t)(row_bytes / 4), value_rows);
+    else
+        page_write_kernel<uint8_t><<<blocks, 256, 0, s>>>(dst_base, (const char *)values, page_ids, offsets,
+                                                          page_count, page_size, (int64_t)row_bytes, value_rows);
+    return check_launch("kv page write");
+}
+
+int puter_hip_kv_page_gather(const void *storage, const int32_t *page_table, void *output,
+                             int64_t page_count, int64_t page_size, int64_t inner,
+                             int64_t out_rows, int64_t storage_offset, int dtype, void *stream) {
+    const int es = dtype_bytes(dtype);
+    if (es == 0) return fail(PUTER_ERR_INVALID, "kv page gather: unsupported dtype %d", dtype);
+    if (page_count < 0 || page_size <= 0 || inner < 0 || out_rows < 0 || storage_offset < 0)
+        return fail(PUTER_ERR_INVALID, "kv page gather: invalid shape");
+    if (out_rows == 0 || inner == 0) return PUTER_OK;
+    if (!storage || !page_table || !output) return fail(PUTER_ERR_NIL, "kv page gather: nil buffer");
+    hipStream_t s = as_stream(stream);
+    const size_t row_bytes = (size_t)inner * es;
+    const char *src = static_cast<const char *>(storage) + (size_t)storage_offset * es;
+    const unsigned blocks = (unsigned)((out_rows + 3) / 4);
+    const void *ptrs[2] = {src, output};
+    if (row_bytes % 16 == 0 && all_aligned(ptrs, 2, 15))
+        page_gather_kernel<uint4><<<blocks, 256, 0, s>>>(src, page_table, (char *)output, page_count,
+                                                         page_size, (int64_t)(row_bytes / 16), out_rows);
+    else if (row_bytes % 4 == 0 && all_aligned(ptrs, 2, 3))
+        page_gather_kernel<uint32_t><<<blocks, 256, 0, s>>>(src, page_table, (char *)output, page_count,
+                                                            page_size, (int64_t)(row_bytes / 4), out_rows);
+    else
+        page_gather_kernel<uint8_t><<<blocks, 256, 0, s>>>(src, page_table, (char *)output, page_count,
+                                                           page_size, (int64_t)row_bytes, out_rows);
+    return check_launch("kv page gather");
+}
+
+}  // extern "C"

@@ -1,0 +1,299 @@
+// RoPE and MultiAxisRoPE.
+// Reference: device/cpu/rope/compute.go:11-330 (angles in float64: theta =
+// pos * base^(-2i/D) (+ Llama-3 wavelength smoothing), cos/sin rounded to f32,
+// rotation e' = e*c - o*s, o' = e*s + o*c in f32, 16-bit RNE store).
+//
+// Layout [seq, heads, D].  One block owns PPB consecutive positions: it first
+// fills an LDS table of (cos, sin) for its positions x D/2 pairs in float64
+// (the angle depends on (position, pair) only, so every head reuses it), then
+// streams the positions' [heads * D] slabs through 16-byte vectors.  Each
+// element is read and written once (4 B/elem in bf16); the float64 work is
+// D/2 sincos per position, not per element.  input may alias output.
+#include "common.hpp"
+
+namespace puter {
+
+struct RopeArgs {
+    const void *in;
+    void *out;
+    int64_t seq, heads, dim;
+    int64_t start;
+    double base, factor, low, high;
+    int64_t orig_ctx;
+    int mode, scaling;
+    int ppb;  // positions per block
+};
+
+__device__ __forceinline__ double rope_inv_freq(const RopeArgs &a, int64_t pair) {
+    // ropeInverseFrequency compute.go:98-107
+    const double exponent = -(double)(2 * pair) / (double)a.dim;
+    const double inv = pow(a.base, exponent);
+    if (a.scaling != 1) return inv;
+    // llama3ScaledInverseFrequency compute.go:109-126
+    const double wavelength = (2.0 * M_PI) / inv;
+    const double lowW = (double)a.orig_ctx / a.low;
+    const double highW = (double)a.orig_ctx / a.high;
+    if (wavelength > lowW) return inv / a.factor;
+    if (wavelength < highW) return inv;
+    const double smooth = ((double)a.orig_ctx / wavelength - a.low) / (a.high - a.low);
+    return (1.0 - smooth) * (inv / a.factor) + smooth * inv;
+}
+
+constexpr int kRopeLds = 8192;  // max (cos, sin) entries per block (64 KiB of LDS)
+
+template <int DT>
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ float2 cs[];
+    const int64_t half = a.dim / 2;
+    const int64_t p0 = (int64_t)blockIdx.x * a.ppb;
+    const int64_t np = min((int64_t)a.ppb, a.seq - p0);
+    for (int64_t t = threadIdx.x; t < np * half; t += blockDim.x) {
+        const int64_t p = t / half, pair = t - p * half;
+        const double theta = (double)(p0 + p + a.start) * rope_inv_freq(a, pair);
+        double sn, cn;
+        sincos(theta, &sn, &cn);
+        cs[t] = make_float2((float)cn, (float)sn);
+    }
+    __syncthreads();
+    using T = typename Elem<DT>::T;
+    constexpr int N = Vec<DT>::N;
+    const int64_t slab = a.heads * a.dim;           // elements per position
+    const T *in = reinterpret_cast<const T *>(a.in) + p0 * slab;
+    T *out = reinterpret_cast<T *>(a.out) + p0 * slab;
+    if (a.mode == 0) {
+        // interleaved pairs (2i, 2i+1): a 16-byte vector holds N/2 whole pairs
+        const int64_t nvec = np * slab / N;
+        for (int64_t v = threadIdx.x; v < nvec; v += blockDim.x) {
+            const int64_t e0 = v * N;
+            const int64_t p = e0 / slab;
+            const int64_t pair0 = (e0 - p * slab) % a.dim / 2;
+            float f[N], o[N];
+            load_vec<DT>(in, (size_t)v, f);
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) {
+                const float2 c = cs[p * half + pair0 + i];
+                const float e = f[2 * i], od = f[2 * i + 1];
+                o[2 * i] = e * c.x - od * c.y;
+                o[2 * i + 1] = e * c.y + od * c.x;
+            }
+            reinterpret_cast<uint4 *>(out)[v] = pack_vec<DT>(o);
+        }
+    } else {
+        // half mode (i, i + D/2): a vector of the first half pairs with the
+        // vector D/2 further on; each thread owns both
+        const int64_t vhalf = half / N;            // vectors per half-row
+        const int64_t nwork = np * a.heads * vhalf;
+        for (int64_t w = threadIdx.x; w < nwork; w += blockDim.x) {
+            const int64_t row = w / vhalf, j = w - row * vhalf;
+            const int64_t p = row / a.heads;
+            const size_t lo = (size_t)(row * a.dim / N + j);
+            const size_t hi = lo + (size_t)vhalf;
+            float e[N], od[N], oe[N], oo[N];
+            load_vec<DT>(in, lo, e);
+            load_vec<DT>(in, hi, od);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const float2 c = cs[p * half + j * N + i];
+                oe[i] = e[i] * c.x - od[i] * c.y;
+                oo[i] = e[i] * c.y + od[i] * c.x;
+            }
+            reinterpret_cast<uint4 *>(out)[lo] = pack_vec<DT>(oe);
+            reinterpret_cast<uint4 *>(out)[hi] = pack_vec<DT>(oo);
+        }
+    }
+}
+
+// Element-wise fallback for shapes the vector path cannot take (odd sizes,
+// unaligned pointers): same table, one pair per thread iteration.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_scalar_kernel(RopeArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ float2 cs[];
+    const int64_t half = a.dim / 2;
+    const int64_t p0 = (int64_t)blockIdx.x * a.ppb;
+    const int64_t np = min((int64_t)a.ppb, a.seq - p0);
+    for (int64_t t = threadIdx.x; t < np * half; t += blockDim.x) {
+        const int64_t p = t / half, pair = t - p * half;
+        const double theta = (double)(p0 + p + a.start) * rope_inv_freq(a, pair);
+        double sn, cn;
+        sincos(theta, &sn, &cn);
+        cs[t] = make_float2((float)cn, (float)sn);
+    }
+    __syncthreads();
+    using T = typename Elem<DT>::T;
+    const T *in = reinterpret_cast<const T *>(a.in);
+    T *out = reinterpret_cast<T *>(a.out);
+    const int64_t npairs = np * a.heads * half;
+    for (int64_t w = threadIdx.x; w < npairs; w += blockDim.x) {
+        const int64_t row = w / half, pair = w - row * half;
+        const int64_t p = row / a.heads;
+        const size_t base = (size_t)((p0 * a.heads + row) * a.dim);
+        const size_t ei = a.mode == 1 ? base + pair : base + 2 * pair;
+        const size_t oi = a.mode == 1 ? base + half + pair : ei + 1;
+        const float2 c = cs[p * half + pair];
+        const float e = Elem<DT>::load(in[ei]), od = Elem<DT>::load(in[oi]);
+        out[ei] = Elem<DT>::store(e * c.x - od * c.y);
+        out[oi] = Elem<DT>::store(e * c.y + od * c.x);
+    }
+}
+
+// MultiAxisRoPE compute.go:195-330: one thread per pair, angle in float64.
+struct MultiAxisArgs {
+    const void *in;
+    void *out;
+    int64_t batch, seq, heads, dim;
+    double base;
+    int64_t latent_seq, latent_side;
+    int axis_count;
+    int64_t starts[5];
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void multi_axis_rope_kernel(MultiAxisArgs a) {
+#pragma clang fp contract(off)
+    using T = typename Elem<DT>::T;
+    const int64_t half = a.dim / 2;
+    const int64_t total = a.batch * a.seq * a.heads * half;
+    const int64_t text_len = max(a.seq - a.latent_seq, (int64_t)0);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t po = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; po < total; po += stride) {
+        const int64_t pair = po % half;
+        const int64_t head = (po / half) % a.heads;
+        const int64_t s = (po / (half * a.heads)) % a.seq;
+        const int64_t b = po / (half * a.heads * a.seq);
+        const size_t even = (size_t)(((b * a.seq + s) * a.heads + head) * a.dim + pair * 2);
+        int axis = 0;
+        int64_t local = pair, axis_pairs = 0;
+        for (int k = 0; k < a.axis_count; ++k) {
+            if (pair < a.starts[k + 1]) {
+                axis = k;
+                local = pair - a.starts[k];
+                axis_pairs = a.starts[k + 1] - a.starts[k];
+                break;
+            }
+        }
+        int64_t position;
+        if (s < text_len) {
+            position = ((a.axis_count == 4 && axis == 3) || (a.axis_count < 4 && axis == 0)) ? s : 0;
+        } else {
+            const int64_t img = s - text_len;
+            position = axis == 1 ? img / a.latent_side : axis == 2 ? img % a.latent_side : 0;
+        }
+        float c = 1.0f, sn = 0.0f;
+        const double axis_dim = (double)(axis_pairs * 2);
+        if (axis_dim != 0) {
+            const double exponent = -2.0 * (double)local / axis_dim;
+            const double angle = (double)position * pow(a.base, exponent);
+            double s64, c64;
+            sincos(angle, &s64, &c64);
+            c = (float)c64;
+            sn = (float)s64;
+        }
+        const T *in = reinterpret_cast<const T *>(a.in);
+        T *out = reinterpret_cast<T *>(a.out);
+        const float e = Elem<DT>::load(in[even]), o = Elem<DT>::load(in[even + 1]);
+        out[even] = Elem<DT>::store(e * c - o * sn);
+        out[even + 1] = Elem<DT>::store(e * sn + o * c);
+    }
+}
+
+template <int DT>
+static int launch_rope(RopeArgs a, hipStream_t s) {
+    constexpr int N = Vec<DT>::N;
+    const int64_t half = a.dim / 2;
+    const int64_t slab = a.heads * a.dim;
+    // ~4096 elements of work per block, bounded by the LDS table
+    int64_t ppb = slab >= 4096 ? 1 : 4096 / slab;
+    if (ppb * half > kRopeLds) ppb = kRopeLds / half;
+    if (ppb < 1) ppb = 1;
+    a.ppb = (int)ppb;
+    const unsigned blocks = (unsigned)((a.seq + ppb - 1) / ppb);
+    const bool vec = aligned16(a.in) && aligned16(a.out) && slab % N == 0 &&
+                     (a.mode == 0 ? (a.dim % N == 0) : (half % N == 0));
+    const size_t lds = (size_t)(ppb * half) * sizeof(float2);
+    if (vec) rope_kernel<DT><<<blocks, 256, lds, s>>>(a);
+    else rope_scalar_kernel<DT><<<blocks, 256, lds, s>>>(a);
+    return check_launch("rope");
+}
+
+}  // namespace puter
+
+using namespace puter;
+
+extern "C" {
+
+int puter_hip_rope(const puter_rope_config *config, const void *input, void *output,
+                   int64_t seq_len, int64_t num_heads, int64_t head_dim, int dtype, void *stream) {
+    if (!config) return fail(PUTER_ERR_NIL, "rope: nil config");
+    if (seq_len < 0 || num_heads < 0 || head_dim < 0) return fail(PUTER_ERR_INVALID, "rope: negative shape");
+    // dispatchRoPE compute.go:17-19: silent no-op
+    if (seq_len == 0 || num_heads == 0 || head_dim == 0 || head_dim % 2 != 0) return PUTER_OK;
+    // RoPEConfig.Validate device/config.go:215-258
+    const puter_rope_config &c = *config;
+    if (!(c.base_freq > 0)) return fail(PUTER_ERR_INVALID, "rope: base frequency must be positive, got %g", c.base_freq);
+    if (c.mode != 0 && c.mode != 1) return fail(PUTER_ERR_INVALID, "rope: unsupported mode %d", c.mode);
+    if (c.scaling != 0 && c.scaling != 1) return fail(PUTER_ERR_INVALID, "rope: unsupported scaling %d", c.scaling);
+    if (c.scaling == 1) {
+        if (!(c.scaling_factor > 0)) return fail(PUTER_ERR_INVALID, "rope: scaling factor must be positive");
+        if (!(c.low_freq_factor > 0)) return fail(PUTER_ERR_INVALID, "rope: low frequency factor must be positive");
+        if (!(c.high_freq_factor > c.low_freq_factor))
+            return fail(PUTER_ERR_INVALID, "rope: high frequency factor must exceed low frequency factor");
+        if (c.original_context <= 0) return fail(PUTER_ERR_INVALID, "rope: original context must be positive");
+    }
+    if (!is_norm_dtype(dtype)) return fail(PUTER_ERR_INVALID, "rope: unsupported dtype %d", dtype);
+    if (head_dim / 2 > kRopeLds) return fail(PUTER_ERR_INVALID, "rope: head_dim %lld too large", (long long)head_dim);
+    if (!input || !output) return fail(PUTER_ERR_NIL, "rope: nil buffer");
+    RopeArgs a{input, output, seq_len, num_heads, head_dim, c.start_position, c.base_freq,
+               c.scaling_factor, c.low_freq_factor, c.high_freq_factor, c.original_context,
+               c.mode, c.scaling, 1};
+    hipStream_t s = as_stream(stream);
+    switch (dtype) {
+    case PUTER_F32: return launch_rope<PUTER_F32>(a, s);
+    case PUTER_BF16: return launch_rope<PUTER_BF16>(a, s);
+    case PUTER_F16: return launch_rope<PUTER_F16>(a, s);
+    }
+    return PUTER_ERR_INVALID;
+}
+
+int puter_hip_multi_axis_rope(const puter_multi_axis_rope_config *config, const void *input,
+                              void *output, int64_t batch, int64_t seq_len, int64_t num_heads,
+                              int64_t head_dim, int dtype, void *stream) {
+    if (!config) return fail(PUTER_ERR_NIL, "multi-axis rope: nil config");
+    if (batch < 0 || seq_len < 0 || num_heads < 0 || head_dim < 0)
+        return fail(PUTER_ERR_INVALID, "multi-axis rope: negative shape");
+    if (batch == 0 || seq_len == 0 || num_heads == 0 || head_dim == 0 || head_dim % 2 != 0) return PUTER_OK;
+    const puter_multi_axis_rope_config &c = *config;
+    // MultiAxisRoPEConfig.Validate / ValidateHeadDim device/config.go:148-213
+    if (!(c.base_freq > 0) || c.latent_seq_len <= 0 || c.latent_side <= 0 || c.axis_count <= 0 || c.axis_count > 4)
+        return fail(PUTER_ERR_INVALID, "multi-axis rope: invalid config");
+    int64_t total = 0;
+    for (int k = 0; k < 4; ++k) {
+        if (k >= c.axis_count) {
+            if (c.axis_dims[k] != 0) return fail(PUTER_ERR_INVALID, "multi-axis rope: inactive axis %d has dimension", k);
+            continue;
+        }
+        if (c.axis_dims[k] <= 0 || c.axis_dims[k] % 2 != 0)
+            return fail(PUTER_ERR_INVALID, "multi-axis rope: axis %d dimension must be positive and even", k);
+        total += c.axis_dims[k];
+    }
+    if (total != head_dim) return fail(PUTER_ERR_INVALID, "multi-axis rope: axis dimensions sum to %lld, head dimension is %lld",
+                                       (long long)total, (long long)head_dim);
+    if (!is_norm_dtype(dtype)) return fail(PUTER_ERR_INVALID, "multi-axis rope: unsupported dtype %d", dtype);
+    if (!input || !output) return fail(PUTER_ERR_NIL, "multi-axis rope: nil buffer");
+    MultiAxisArgs a{input, output, batch, seq_len, num_heads, head_dim, c.base_freq,
+                    c.latent_seq_len, c.latent_side, c.axis_count, {0, 0, 0, 0, 0}};
+    for (int k = 0; k < c.axis_count; ++k) a.starts[k + 1] = a.starts[k] + c.axis_dims[k] / 2;
+    const int64_t pairs = batch * seq_len * num_heads * (head_dim / 2);
+    int64_t blocks = (pairs + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipStream_t s = as_stream(stream);
+    switch (dtype) {
+    case PUTER_F32: multi_axis_rope_kernel<PUTER_F32><<<(unsigned)blocks, 256, 0, s>>>(a); break;
+    case PUTER_BF16: multi_axis_rope_kernel<PUTER_BF16><<<(unsigned)blocks, 256, 0, s>>>(a); break;
+    case PUTER_F16: multi_axis_rope_kernel<PUTER_F16><<<(unsigned)blocks, 256, 0, s>>>(a); break;
+    }
+    return check_launch("multi-axis rope");
+}
+
+}  // extern "C"

@@ -1,0 +1,73 @@
+"""Shared test helpers: seeded inputs, host<->device moves, parity metrics.
+
+Parity bars (north star): bit-exact for casts and page gathers; otherwise
+  normwise   ||gpu - ref||_inf / ||ref||_inf  <= tol
+  elementwise |gpu - ref| / max(|ref|, floor * ||ref||_inf) <= tol
+with tol = 1e-5 for f32 and 1e-2 for bf16 / fp8.  `floor` is 1e-3 for
+element-wise kernels (norms, RoPE, activations) and 1e-2 for attention, whose
+outputs are sums over thousands of keys (a value 1e-3 of the row maximum is
+cancellation noise of the softmax-weighted sum).
+"""
+import numpy as np
+
+import oracle as O
+
+TOL = {O.F32: 1e-5, O.F16: 1e-3, O.BF16: 1e-2, O.F8E4M3: 1e-2}
+
+
+def seeded(seed, shape, mean=0.0, std=1.0):
+    n = int(np.prod(shape))
+    return O.normal(seed, n, mean, std).reshape(shape)
+
+
+def encode(x32, dtype):
+    """f32 numpy -> storage numpy (bits for 16/8-bit formats)."""
+    return x32.astype(np.float32) if dtype == O.F32 else O.from_f32(x32, dtype)
+
+
+def decode(bits, dtype):
+    return bits.astype(np.float32) if dtype == O.F32 else O.to_f32(bits, dtype)
+
+
+def to_dev(arr):
+    import torch
+    arr = np.ascontiguousarray(arr)
+    if arr.dtype == np.uint16:
+        t = torch.from_numpy(arr.view(np.int16))
+    elif arr.dtype == np.uint8:
+        t = torch.from_numpy(arr)
+    else:
+        t = torch.from_numpy(arr)
+    return t.cuda()
+
+
+def empty_dev(shape, np_dtype):
+    import torch
+    table = {np.float32: torch.float32, np.uint16: torch.int16, np.uint8: torch.uint8,
+             np.int32: torch.int32}
+    return torch.empty(tuple(shape), dtype=table[np.dtype(np_dtype).type], device="cuda")
+
+
+def to_host(t, np_dtype):
+    import torch
+    torch.cuda.synchronize()
+    a = t.cpu().numpy()
+    return a.view(np_dtype) if a.dtype != np_dtype else a
+
+
+def errors(got, ref, floor=1e-3):
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    scale = np.max(np.abs(ref)) if ref.size else 0.0
+    if scale == 0:
+        return float(np.max(np.abs(got - ref), initial=0.0)), 0.0
+    norm = float(np.max(np.abs(got - ref)) / scale)
+    elem = float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), floor * scale)))
+    return norm, elem
+
+
+def assert_close(got, ref, tol, floor=1e-3, what=""):
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    norm, elem = errors(got, ref, floor)
+    assert norm <= tol and elem <= tol, f"{what}: normwise {norm:.3e}, elementwise {elem:.3e} > {tol}"
+    return norm, elem

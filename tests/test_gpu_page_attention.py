@@ -1,0 +1,184 @@
+"""GPU parity: paged KV write/gather (bit-exact), multi-head attention, paged
+decode and the f32 matmul against the CPU oracle.
+
+Reference: device/cpu/shape/page_generic.go, execution/page_intrinsic.go,
+device/cpu/attention/{compute,typed_compute,softmax}.go, device/cpu/matmul."""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import TOL, assert_close, decode, empty_dev, encode, seeded, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+NP = {O.F32: np.float32, O.F16: np.uint16, O.BF16: np.uint16, O.F8E4M3: np.uint8}
+
+
+# -------------------------------------------------------------- paged KV --
+def test_page_write_reference_kat(backend):
+    """execution/page_intrinsic_test.go:15-71: storage [2,3,2,1,1] f32, layer 1
+    (storageOffset 6), rows 7, 8 -> page 1 slots 0, 1 -> storage[8]=7, [9]=8."""
+    storage = to_dev(np.zeros(12, np.float32))
+    values = to_dev(np.array([7, 8], np.float32))
+    ids = to_dev(np.array([1, 1], np.int32))
+    offs = to_dev(np.array([0, 1], np.int32))
+    backend.KVPageWrite(storage, values, ids, offs, storage, 3, 2, 1, 2, 6, O.F32)
+    got = to_host(storage, np.float32)
+    expect = np.zeros(12, np.float32)
+    expect[8], expect[9] = 7, 8
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("dt,inner", [(O.BF16, 1024), (O.F32, 24), (O.F16, 3), (O.F8E4M3, 1024), (O.BF16, 7)])
+def test_page_write_gather_roundtrip(backend, dt, inner):
+    rng = np.random.default_rng(inner + dt)
+    pages, ps = 40, 16
+    es = np.dtype(NP[dt]).itemsize
+    storage = rng.integers(0, 2**(8 * es) if es < 4 else 2**31, size=pages * ps * inner).astype(
+        np.uint32 if es == 4 else NP[dt])
+    if es == 4:
+        storage = storage.view(np.float32)
+    rows = 37
+    ids = rng.integers(0, pages, rows).astype(np.int32)
+    offs = rng.integers(0, ps, rows).astype(np.int32)
+    # distinct slots so the write order cannot matter
+    slots = np.unique(ids.astype(np.int64) * ps + offs, return_index=True)[1]
+    ids, offs = ids[slots], offs[slots]
+    vals = rng.integers(0, 200, size=ids.size * inner).astype(NP[dt] if es < 4 else np.float32)
+    ref_store = O.page_write(storage, vals, ids, offs, ps, inner)
+    d_store = to_dev(storage)
+    backend.KVPageWrite(d_store, to_dev(vals), to_dev(ids), to_dev(offs), d_store, pages, ps, inner,
+                        ids.size, 0, dt)
+    got_store = to_host(d_store, storage.dtype)
+    assert np.array_equal(got_store.view(np.uint8), ref_store.view(np.uint8))
+    table = rng.permutation(pages)[:9].astype(np.int32)
+    out_rows = 9 * ps - 5
+    ref = O.page_gather(ref_store, table, ps, inner, out_rows)
+    out = empty_dev((out_rows, inner), storage.dtype)
+    backend.KVPageGather(d_store, to_dev(table), out, pages, ps, inner, out_rows, 0, dt)
+    got = to_host(out, storage.dtype)
+    assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+
+
+def test_page_gather_identity_table_is_contiguous_copy(backend):
+    pages, ps, inner = 8, 4, 32
+    storage = seeded(3, (pages * ps * inner,))
+    out = empty_dev((pages * ps, inner), np.float32)
+    backend.KVPageGather(to_dev(storage), to_dev(np.arange(pages, dtype=np.int32)), out, pages, ps,
+                         inner, pages * ps, 0, O.F32)
+    assert np.array_equal(to_host(out, np.float32).ravel(), storage)
+
+
+def test_page_out_of_range_ids_never_touch_memory(backend):
+    pages, ps, inner = 4, 2, 8
+    storage = seeded(4, (pages * ps * inner,))
+    d = to_dev(storage)
+    backend.KVPageWrite(d, to_dev(np.ones(2 * inner, np.float32)), to_dev(np.array([9, -1], np.int32)),
+                        to_dev(np.array([0, 0], np.int32)), d, pages, ps, inner, 2, 0, O.F32)
+    assert np.array_equal(to_host(d, np.float32), storage)   # both rows skipped
+    out = empty_dev((2 * ps, inner), np.float32)
+    backend.KVPageGather(d, to_dev(np.array([1, 77], np.int32)), out, pages, ps, inner, 2 * ps, 0, O.F32)
+    got = to_host(out, np.float32)
+    assert np.array_equal(got[:ps].ravel(), storage[ps * inner:2 * ps * inner])
+    assert np.all(got[ps:] == 0)
+
+
+# -------------------------------------------------------------- attention --
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("sq,sk,h,kvh,d,causal", [
+    (128, 128, 8, 8, 64, True),     # config 1
+    (77, 77, 4, 2, 64, True),
+    (5, 300, 4, 1, 128, True),       # bottom-right aligned causal
+    (64, 64, 8, 2, 128, False),
+    (1, 513, 8, 2, 128, True),       # decode shape
+])
+def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
+    import puter_amd
+    std = 1.0 / np.sqrt(d) if dt != O.F32 else 1.0
+    q = encode(seeded(90 + sq, (sq, h * d), 0.0, std), dt)
+    k = encode(seeded(91 + sk, (sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(92 + sk, (sk, kvh * d)), dt)
+    ref = decode(O.mha(q, k, v, h, d, causal=causal, kv_heads=kvh, dtype=dt), dt)
+    out = empty_dev((sq, h * d), NP[dt])
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, 0, 0.0, kvh)
+    backend.MultiHeadAttention(cfg, to_dev(q), to_dev(k), to_dev(v), out, sq, sk, dt)
+    assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], floor=1e-2, what="mha")
+
+
+def test_mha_window_alibi(backend):
+    import puter_amd
+    dt, sq, h, d = O.F32, 40, 2, 32
+    q, k, v = (seeded(s, (sq, h * d)) for s in (1, 2, 3))
+    ref = O.mha(q, k, v, h, d, causal=True, kv_heads=0, window=7, alibi=0.25, dtype=dt)
+    out = empty_dev((sq, h * d), np.float32)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, True, 7, 0.25, 0)
+    backend.MultiHeadAttention(cfg, to_dev(q), to_dev(k), to_dev(v), out, sq, sq, dt)
+    assert_close(to_host(out, np.float32), ref, TOL[dt], floor=1e-2, what="window+alibi")
+
+
+def test_mha_batched_prefill_bf16(backend):
+    import puter_amd
+    dt, b, s, h, kvh, d = O.BF16, 2, 256, 8, 2, 128
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(7, (b, s, h * d), 0.0, std), dt)
+    k = encode(seeded(8, (b, s, kvh * d), 0.0, std), dt)
+    v = encode(seeded(9, (b, s, kvh * d), 0.0, std), dt)
+    out = empty_dev((b, s, h * d), np.uint16)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, True, 0, 0.0, kvh)
+    backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, s, s, dt)
+    got = decode(to_host(out, np.uint16), dt)
+    for i in range(b):
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=True, kv_heads=kvh, dtype=dt), dt)
+        assert_close(got[i], ref, TOL[dt], floor=1e-2, what=f"batch {i}")
+
+
+def paged_case(seed, batch, ctx_lo, ctx_hi, ps, h, kvh, d, kv_dt):
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(ctx_lo, ctx_hi + 1, batch).astype(np.int32)
+    npages = (ctx + ps - 1) // ps
+    total = int(npages.sum())
+    perm = rng.permutation(total).astype(np.int32)
+    max_pages = int(npages.max())
+    table = np.zeros((batch, max_pages), np.int32)
+    at = 0
+    for i in range(batch):
+        table[i, :npages[i]] = perm[at:at + npages[i]]
+        at += npages[i]
+    q = O.from_f32(seeded(seed + 1, (batch, h * d)), O.BF16)
+    kf = seeded(seed + 2, (total, ps, kvh, d))
+    vf = seeded(seed + 3, (total, ps, kvh, d))
+    if kv_dt == O.BF16:
+        kp, vp, ks, vs = O.from_f32(kf, O.BF16), O.from_f32(vf, O.BF16), None, None
+    else:
+        ks = (np.abs(kf).reshape(-1, kvh, d).max(axis=(0, 2)) / 448.0).astype(np.float32)
+        vs = (np.abs(vf).reshape(-1, kvh, d).max(axis=(0, 2)) / 448.0).astype(np.float32)
+        kp = O.from_f32((kf / ks[None, None, :, None]).astype(np.float32), O.F8E4M3)
+        vp = O.from_f32((vf / vs[None, None, :, None]).astype(np.float32), O.F8E4M3)
+    return ctx, table, total, q, kp, vp, ks, vs
+
+
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("batch,lo,hi,ps", [(3, 1, 40, 16), (4, 500, 1300, 16), (2, 256, 256, 16)])
+def test_paged_decode(backend, kv_dt, batch, lo, hi, ps):
+    h, kvh, d = 32, 8, 128
+    ctx, table, total, q, kp, vp, ks, vs = paged_case(batch * 100 + lo, batch, lo, hi, ps, h, kvh, d, kv_dt)
+    ref = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, kv_dt, ks, vs)
+    max_ctx = int(ctx.max())
+    ws_bytes = backend.PagedDecodeWorkspaceBytes(batch, h, d, max_ctx)
+    ws = empty_dev((ws_bytes // 4,), np.float32)
+    out = empty_dev((batch, h * d), np.uint16)
+    backend.PagedDecodeAttention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(table), to_dev(ctx), batch,
+                                 table.shape[1], ps, total, h, kvh, d, max_ctx,
+                                 None if ks is None else to_dev(ks), None if vs is None else to_dev(vs),
+                                 kv_dt, out, ws, ws_bytes)
+    assert_close(O.to_f32(to_host(out, np.uint16), O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
+                 floor=1e-2, what="paged decode")
+
+
+def test_matmul_f32(backend):
+    for rows, inner, cols in [(128, 512, 512), (7, 13, 5), (65, 64, 130)]:
+        a = seeded(rows, (rows, inner))
+        b = seeded(cols + 1, (inner, cols), 0.0, 0.02)
+        ref = O.matmul_f32(a, b)
+        out = empty_dev((rows, cols), np.float32)
+        backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, O.F32)
+        assert_close(to_host(out, np.float32), ref, TOL[O.F32], floor=1e-2, what="matmul")
