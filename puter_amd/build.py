@@ -23,6 +23,9 @@ SOURCES = ["runtime.hip", "cast.hip", "norm.hip", "rope.hip", "gated.hip", "page
 HIPFLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-fvisibility=hidden",
+    # no implicit FMA contraction: every float expression rounds per operation
+    # as the reference's Go code does on amd64 (explicit fmaf stays fused)
+    "-ffp-contract=off",
     # packed-FP32 VALU ops stay disabled (known-bad on this pool)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-result", "-Wno-unused-variable",

@@ -12,8 +12,6 @@
 
 namespace puter {
 
-#pragma clang fp contract(off)
-
 __device__ __forceinline__ float fast_exp32(float x) {
     // device/cpu/math/f32.go:21-46
     if (x < -87.33654f) return 0.0f;
