@@ -9,22 +9,9 @@
 // online softmax over 256-key chunks staged in LDS, f32 accumulation) and the
 // dispatch: bf16 causal/non-causal prefill with D in {64, 128} and no
 // window/ALiBi goes to the MFMA flash kernel (prefill.hip).
-#include "common.hpp"
+#include "attention.hpp"
 
 namespace puter {
-
-struct MhaArgs {
-    const void *q, *k, *v;
-    void *o;
-    int64_t batch, seq_q, seq_k, heads, kv_heads, dim;
-    int causal;
-    int64_t window;
-    float alibi;
-    float scale;
-};
-
-// Defined in prefill.hip: returns true if it launched.
-bool launch_prefill_mfma(const MhaArgs &a, int dtype, hipStream_t s, int *status);
 
 template <int DT>
 __global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {

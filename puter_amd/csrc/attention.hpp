@@ -1,0 +1,23 @@
+// Shared argument block of the attention kernels (attention.hip dispatches,
+// prefill.hip holds the MFMA flash kernel).
+#pragma once
+
+#include "common.hpp"
+
+namespace puter {
+
+struct MhaArgs {
+    const void *q, *k, *v;
+    void *o;
+    int64_t batch, seq_q, seq_k, heads, kv_heads, dim;
+    int causal;
+    int64_t window;
+    float alibi;
+    float scale;
+};
+
+// MFMA bf16 flash prefill (prefill.hip).  Returns true and sets *status when
+// the shape is one it serves (bf16, head_dim 128, no window / ALiBi).
+bool launch_prefill_mfma(const MhaArgs &a, int dtype, hipStream_t s, int *status);
+
+}  // namespace puter

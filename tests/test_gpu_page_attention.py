@@ -132,6 +132,32 @@ def test_mha_batched_prefill_bf16(backend):
         assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"batch {i}")
 
 
+@pytest.mark.parametrize("b,sq,sk,h,kvh,causal", [
+    (1, 1024, 1024, 8, 2, True),    # several diagonal and full tiles per block
+    (2, 333, 333, 4, 1, True),      # ragged: partial query and key tiles
+    (1, 200, 520, 4, 4, True),      # seqK > seqQ: bottom-right aligned causal window
+    (1, 130, 77, 8, 8, False),      # non-causal, seqK < 64-key tile
+    (1, 96, 40, 4, 2, True),        # seqQ > seqK: leading queries see no key -> zeros
+])
+def test_prefill_mfma_shapes(backend, b, sq, sk, h, kvh, causal):
+    import puter_amd
+    dt, d = O.BF16, 128
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(300 + sq, (b, sq, h * d), 0.0, std), dt)
+    k = encode(seeded(301 + sk, (b, sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(302 + sk, (b, sk, kvh * d)), dt)
+    out = empty_dev((b, sq, h * d), np.uint16)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, 0, 0.0, kvh)
+    backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, sq, sk, dt)
+    got = decode(to_host(out, np.uint16), dt)
+    O.set_threads(8)
+    for i in range(b):
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, dtype=dt), dt)
+        assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"prefill batch {i}")
+        if causal and sq > sk:   # rows with no visible key are exactly zero, as softmax.go:50-56
+            assert np.all(got[i][:sq - sk] == 0)
+
+
 def paged_case(seed, batch, ctx_lo, ctx_hi, ps, h, kvh, d, kv_dt):
     rng = np.random.default_rng(seed)
     ctx = rng.integers(ctx_lo, ctx_hi + 1, batch).astype(np.int32)
