@@ -236,12 +236,42 @@ def cpu_baseline():
             "sample": f"oracle fused GatedResidual+RMSNorm bf16, {rows}x{h}, {reps} reps in {el:.1f}s"}
 
 
+def profile_dominant(torch, be, puter, launches):
+    """Counter-collection workload: the dominant kernel (fused GatedResidual +
+    RMSNorm, 65536 x 8192 bf16) `launches` times, then a plain device copy of
+    1 GiB (torch copy_) whose FETCH_SIZE / WRITE_SIZE calibrate the counters
+    (its algorithmic traffic is exactly 1 GiB read + 1 GiB written)."""
+    rows, h = max(ROWS), max(HIDDEN)
+    n = rows * h
+    bf = torch.bfloat16
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
+    res = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+    br = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+    hid = torch.empty(n, device="cuda", dtype=bf)
+    out = torch.empty(n, device="cuda", dtype=bf)
+    mod = torch.randn(3 * h, device="cuda", dtype=bf, generator=gen)
+    gamma = torch.ones(h, device="cuda", dtype=bf)
+    cfg = puter.RMSNormConfig(1e-5)
+    for _ in range(launches):
+        be.GatedResidualRMSNorm(cfg, res, br, mod, gamma, hid, out, rows, h, rows, 3 * h, 0, puter.BF16)
+    src = torch.empty(1 << 28, device="cuda", dtype=torch.float32)   # 1 GiB
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    for _ in range(launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile workload done: {launches} x fused GR+RMSNorm {rows}x{h} bf16 "
+        f"({8 * n} B algorithmic each), {launches} x 1 GiB copy")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default="norm,rope,prefill,decode,cpu")
+    ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
+                    help="only run the dominant kernel N times plus a 1 GiB calibration copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -250,10 +280,20 @@ def main():
     import torch
     import puter_amd as puter
     be = puter.Backend()
+    if args.profile_dominant:
+        profile_dominant(torch, be, puter, args.profile_dominant)
+        return
     only = set(args.only.split(","))
     ms, step_bytes, per, roof = norm_sweep(torch, be, puter, args.steps, args.warmup)
     log(f"norm sweep: {ms:.3f} ms/step, {step_bytes / (ms * 1e-3) / 1e9:.1f} GB/s")
     configs = {"norm_sweep_GBs": per}
+    # context: a device-to-device copy of 1 GiB (read 1 GiB + write 1 GiB)
+    src = torch.empty(1 << 28, device="cuda", dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    t = Timer(torch).time(lambda: dst.copy_(src), 10)
+    configs["copy_1GiB_GBs"] = round(2 * (1 << 30) / (t * 1e-3) / 1e9, 1)
+    del src, dst
+    torch.cuda.empty_cache()
     if "rope" in only:
         configs.update(rope_swiglu_casts(torch, be, puter))
         log(f"rope/swiglu/casts: {configs}")

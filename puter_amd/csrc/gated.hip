@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void unary_kernel(void *__restrict__ dst,
 
 static unsigned grid_for(int64_t units) {
     int64_t b = (units + 255) / 256;
-    if (b > 16384) b = 16384;
+    if (b > (1 << 20)) b = 1 << 20;
     if (b < 1) b = 1;
     return (unsigned)b;
 }

@@ -57,22 +57,24 @@ __device__ __forceinline__ void prefill_load_tile(const PrefillArgs &a, const ui
                                                   uint4 (&kr)[4], uint4 (&vr)[4]) {
     using namespace fa;
     const int64_t rs = (int64_t)a.kv_heads * D;  // row stride of K/V in elements
+    // Keys past the end are clamped to the last row (branch-free loads): their
+    // scores are masked to -inf, so they contribute p = 0 times finite data.
+    const int last = a.seq_k - 1;
     // K: 64 rows x 16 chunks of 16 B; thread takes chunks tid + 256*i
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int c = tid + 256 * i;
         const int row = c >> 4, col = c & 15;
-        const int key = kv0 + row;
-        kr[i] = key < a.seq_k ? *reinterpret_cast<const uint4 *>(kbase + (int64_t)key * rs + col * 8)
-                              : make_uint4(0, 0, 0, 0);
+        const int key = min(kv0 + row, last);
+        kr[i] = *reinterpret_cast<const uint4 *>(kbase + (int64_t)key * rs + col * 8);
     }
-    // V: thread takes keys kb*4 .. +3 of the 8 dims db*8 .. +7
-    const int db = tid & 15, kb = tid >> 4;
+    // V: thread takes keys kb*4 .. +3 of the 8 dims db*8 .. +7.  Lanes of a
+    // wave vary kb fastest so the transposed LDS writes below hit distinct banks.
+    const int kb = tid & 15, db = tid >> 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int key = kv0 + kb * 4 + i;
-        vr[i] = key < a.seq_k ? *reinterpret_cast<const uint4 *>(vbase + (int64_t)key * rs + db * 8)
-                              : make_uint4(0, 0, 0, 0);
+        const int key = min(kv0 + kb * 4 + i, last);
+        vr[i] = *reinterpret_cast<const uint4 *>(vbase + (int64_t)key * rs + db * 8);
     }
 }
 
@@ -85,18 +87,20 @@ __device__ __forceinline__ void prefill_store_tile(uint16_t *ks, uint16_t *vt, i
         const int row = c >> 4, col = c & 15;
         *reinterpret_cast<uint4 *>(ks + row * KS + col * 8) = kr[i];
     }
-    // transpose 4 keys x 8 dims into V^T rows: one 8-byte write per dim
-    const int db = tid & 15, kb = tid >> 4;
+    // transpose 4 keys x 8 dims into V^T rows: one 8-byte write per dim; the
+    // 16 lanes of a write pass differ in kb -> consecutive 8-byte slots of one row
+    const int kb = tid & 15, db = tid >> 4;
     const uint32_t w[4][4] = {{vr[0].x, vr[0].y, vr[0].z, vr[0].w}, {vr[1].x, vr[1].y, vr[1].z, vr[1].w},
                               {vr[2].x, vr[2].y, vr[2].z, vr[2].w}, {vr[3].x, vr[3].y, vr[3].z, vr[3].w}};
 #pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-        const int half = dd & 1, word = dd >> 1;
-        uint32_t e[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = half ? (w[i][word] >> 16) : (w[i][word] & 0xFFFFu);
-        uint2 packed = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
-        *reinterpret_cast<uint2 *>(vt + (db * 8 + dd) * VS + kb * 4) = packed;
+    for (int word = 0; word < 4; ++word) {
+        // v_perm_b32: low halves of keys (0,1) / (2,3) -> dim 2*word, high halves -> dim 2*word+1
+        const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][word], w[0][word], 0x05040100u),
+                                    __builtin_amdgcn_perm(w[3][word], w[2][word], 0x05040100u));
+        const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][word], w[0][word], 0x07060302u),
+                                    __builtin_amdgcn_perm(w[3][word], w[2][word], 0x07060302u));
+        *reinterpret_cast<uint2 *>(vt + (db * 8 + 2 * word) * VS + kb * 4) = lo;
+        *reinterpret_cast<uint2 *>(vt + (db * 8 + 2 * word + 1) * VS + kb * 4) = hi;
     }
 }
 
@@ -108,23 +112,29 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
 
-    // block -> (query tile heaviest first, batch, head)
-    const int bh = a.batch * a.heads;
+    // block -> (query tile, batch, head)
     const int id = blockIdx.x;
-    const int qt = a.causal ? (a.qtiles - 1 - id / bh) : (id / bh);
-    int j = id % bh, b, h;
+    int qt, b, h;
     if (a.xcd_map) {
-        // group = (batch, kv head); its G query heads share K/V -> same XCD
-        const int G = a.heads / a.kv_heads, ngroups = a.batch * a.kv_heads;
+        // Query tiles go heaviest first over the whole grid.  Inside one tile
+        // index, consecutive block ids (dispatched round-robin over the 8
+        // XCDs) are mapped so the G query heads of a kv group (batch, kv head)
+        // land on the same XCD and share its L2 for their K/V tiles.  (Walking
+        // one group at a time per XCD measured slower: it loses the global
+        // heaviest-first order.)
+        const int bh = a.batch * a.heads;
+        const int G = a.heads / a.kv_heads;
+        qt = a.causal ? (a.qtiles - 1 - id / bh) : (id / bh);
+        const int j = id % bh;
         const int xcd = j & 7, slot = j >> 3;
         const int grp = (slot / G) * 8 + xcd;
-        const int hig = slot % G;
         b = grp / a.kv_heads;
-        h = (grp % a.kv_heads) * G + hig;
-        (void)ngroups;
+        h = (grp % a.kv_heads) * G + slot % G;
     } else {
-        b = j / a.heads;
-        h = j % a.heads;
+        const int bh = a.batch * a.heads;
+        qt = a.causal ? (a.qtiles - 1 - id / bh) : (id / bh);
+        b = (id % bh) / a.heads;
+        h = id % a.heads;
     }
     const int kvh = h / (a.heads / a.kv_heads);
     const int q0 = qt * BM;
@@ -138,12 +148,10 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
     const int qw0 = q0 + wave * 32;
     const int qi = qw0 + l32;
     bf16x8 qf[8];
+    const int qload = min(qi, a.seq_q - 1);  // rows past the end compute garbage, never stored
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        uint4 u = qi < a.seq_q ? *reinterpret_cast<const uint4 *>(qbase + (int64_t)qi * qrs + 16 * t + 8 * g)
-                               : make_uint4(0, 0, 0, 0);
-        qf[t] = __builtin_bit_cast(bf16x8, u);
-    }
+    for (int t = 0; t < 8; ++t)
+        qf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(qbase + (int64_t)qload * qrs + 16 * t + 8 * g));
 
     // key range of the block
     int kend = a.seq_k;
@@ -156,17 +164,22 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
     float m = -INFINITY, lsum = 0.0f;
     const int q_last_wave = min(qw0 + 31, a.seq_q - 1);
 
-    uint4 kr[4], vr[4];
     if (ntiles > 0) {
-        prefill_load_tile(a, kbase, vbase, 0, tid, kr, vr);
-        prefill_store_tile(k_lds[0], v_lds[0], tid, kr, vr);
+        uint4 kr0[4], vr0[4];
+        prefill_load_tile(a, kbase, vbase, 0, tid, kr0, vr0);
+        prefill_store_tile(k_lds[0], v_lds[0], tid, kr0, vr0);
     }
     __syncthreads();
 
     for (int it = 0; it < ntiles; ++it) {
         const int kv0 = it * BN;
         const int buf = it & 1;
-        if (it + 1 < ntiles) prefill_load_tile(a, kbase, vbase, kv0 + BN, tid, kr, vr);
+        // next tile's loads go out before the compute and land in registers
+        // that live only inside this iteration (unconditional: the last
+        // iteration re-reads its own tile, which is cheaper than a branch
+        // around the loads)
+        uint4 kr[4], vr[4];
+        prefill_load_tile(a, kbase, vbase, min(kv0 + BN, (ntiles - 1) * BN), tid, kr, vr);
 
         // waves whose queries all precede this tile (causal) skip it
         const bool active = !a.causal || kv0 <= q_last_wave + off;
@@ -174,16 +187,14 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
             const uint16_t *ks = k_lds[buf];
             const uint16_t *vt = v_lds[buf];
             // S^T chunks: keys kv0 + 32c + (8*(r/4) + 4g + r%4), query qi
-            f32x16 s[2];
+            f32x16 s[2] = {(f32x16){}, (f32x16){}};
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                s[c] = (f32x16){};
+            for (int t = 0; t < 8; ++t)     // two independent accumulation chains interleaved
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
+                for (int c = 0; c < 2; ++c) {
                     const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + (32 * c + l32) * KS + 16 * t + 8 * g);
                     s[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], s[c], 0, 0, 0);
                 }
-            }
             const bool need_mask = (kv0 + BN > a.seq_k) || (a.causal && kv0 + BN - 1 > qw0 + off);
             if (need_mask) {
 #pragma unroll
@@ -218,17 +229,19 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
                         pf[c][t][jj] = (__bf16)p;
                     }
             lsum = lsum * alpha + psum;
+            // (a wave-uniform skip of this rescale measured slower: the branch
+            // splits the block and stops MFMA/VALU interleaving)
 #pragma unroll
             for (int d = 0; d < 4; ++d)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
-            // O^T[d, q] += V^T[d, keys] . P^T[keys, q]
+            // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; four independent chains
 #pragma unroll
-            for (int d = 0; d < 4; ++d)
+            for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int c = 0; c < 2; ++c)
+                for (int t = 0; t < 2; ++t)
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
+                    for (int d = 0; d < 4; ++d) {
                         const uint16_t *row = vt + (32 * d + l32) * VS + 32 * c + 16 * t + 4 * g;
                         const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(row);
                         const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(row + 8);
@@ -249,9 +262,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
         for (int d = 0; d < 4; ++d)
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
-                uint32_t w0 = f32_to_bf16(o[d][4 * rb + 0] * inv) | (f32_to_bf16(o[d][4 * rb + 1] * inv) << 16);
-                uint32_t w1 = f32_to_bf16(o[d][4 * rb + 2] * inv) | (f32_to_bf16(o[d][4 * rb + 3] * inv) << 16);
-                *reinterpret_cast<uint2 *>(orow + 32 * d + 8 * rb + 4 * g) = make_uint2(w0, w1);
+                // v_cvt_pk_bf16_f32: round-to-nearest-even, as the software rule
+                bf16x4 v;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = (__bf16)(o[d][4 * rb + i] * inv);
+                *reinterpret_cast<bf16x4 *>(orow + 32 * d + 8 * rb + 4 * g) = v;
             }
     }
 }

@@ -40,6 +40,87 @@ __device__ __forceinline__ double rope_inv_freq(const RopeArgs &a, int64_t pair)
 }
 
 constexpr int kRopeLds = 8192;  // max (cos, sin) entries per block (64 KiB of LDS)
+constexpr int kRopeVpt = 8;     // 16-byte vectors per thread in the register-resident kernel
+
+// Register-resident variant (a block's slab <= 256 * kRopeVpt vectors): every
+// thread issues its loads first, so the float64 angle table is computed while
+// the data is in flight; then one barrier, rotate, store.  MODE 0 interleaved,
+// 1 half.
+template <int DT, int MODE>
+__global__ __launch_bounds__(256) void rope_reg_kernel(RopeArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ float2 cs[];
+    using T = typename Elem<DT>::T;
+    constexpr int N = Vec<DT>::N;
+    const int64_t half = a.dim / 2;
+    const int64_t p0 = (int64_t)blockIdx.x * a.ppb;
+    const int64_t np = min((int64_t)a.ppb, a.seq - p0);
+    const int64_t slab = a.heads * a.dim;
+    const uint4 *in = reinterpret_cast<const uint4 *>(reinterpret_cast<const T *>(a.in) + p0 * slab);
+    uint4 *out = reinterpret_cast<uint4 *>(reinterpret_cast<T *>(a.out) + p0 * slab);
+    const int tid = threadIdx.x;
+    const int64_t vhalf = half / N;
+    // MODE 0: item k = vector tid + 256k.  MODE 1: item k = (lo, hi) vector pair
+    const int64_t nitems = MODE == 0 ? np * slab / N : np * a.heads * vhalf;
+    constexpr int ITEMS = MODE == 0 ? kRopeVpt : kRopeVpt / 2;
+    uint4 lo[ITEMS], hi[ITEMS];
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+        const int64_t w = tid + 256 * k;
+        if (w < nitems) {
+            if constexpr (MODE == 0) {
+                lo[k] = ld_stream(in + w);
+            } else {
+                const int64_t row = w / vhalf, j = w - row * vhalf;
+                const int64_t v = row * a.dim / N + j;
+                lo[k] = ld_stream(in + v);
+                hi[k] = ld_stream(in + v + vhalf);
+            }
+        }
+    }
+    for (int64_t t = tid; t < np * half; t += 256) {
+        const int64_t p = t / half, pair = t - p * half;
+        const double theta = (double)(p0 + p + a.start) * rope_inv_freq(a, pair);
+        double sn, cn;
+        sincos(theta, &sn, &cn);
+        cs[t] = make_float2((float)cn, (float)sn);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+        const int64_t w = tid + 256 * k;
+        if (w >= nitems) continue;
+        if constexpr (MODE == 0) {
+            const int64_t e0 = w * N;
+            const int64_t p = e0 / slab;
+            const int64_t pair0 = (e0 - p * slab) % a.dim / 2;
+            float f[N], o[N];
+            unpack_vec<DT>(lo[k], f);
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) {
+                const float2 c = cs[p * half + pair0 + i];
+                o[2 * i] = f[2 * i] * c.x - f[2 * i + 1] * c.y;
+                o[2 * i + 1] = f[2 * i] * c.y + f[2 * i + 1] * c.x;
+            }
+            st_stream(pack_vec<DT>(o), out + w);
+        } else {
+            const int64_t row = w / vhalf, j = w - row * vhalf;
+            const int64_t p = row / a.heads;
+            const int64_t v = row * a.dim / N + j;
+            float e[N], od[N], oe[N], oo[N];
+            unpack_vec<DT>(lo[k], e);
+            unpack_vec<DT>(hi[k], od);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const float2 c = cs[p * half + j * N + i];
+                oe[i] = e[i] * c.x - od[i] * c.y;
+                oo[i] = e[i] * c.y + od[i] * c.x;
+            }
+            st_stream(pack_vec<DT>(oe), out + v);
+            st_stream(pack_vec<DT>(oo), out + v + vhalf);
+        }
+    }
+}
 
 template <int DT>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
@@ -203,14 +284,27 @@ static int launch_rope(RopeArgs a, hipStream_t s) {
     constexpr int N = Vec<DT>::N;
     const int64_t half = a.dim / 2;
     const int64_t slab = a.heads * a.dim;
+    const bool vec = aligned16(a.in) && aligned16(a.out) && slab % N == 0 &&
+                     (a.mode == 0 ? (a.dim % N == 0) : (half % N == 0));
+    const int64_t slab_vec = slab / N;
+    if (vec && slab_vec <= 256 * kRopeVpt) {
+        // as many positions per block as fill the registers, bounded by the table
+        int64_t ppb = (256 * kRopeVpt) / slab_vec;
+        if (ppb * half > kRopeLds) ppb = kRopeLds / half;
+        if (ppb < 1) ppb = 1;
+        a.ppb = (int)ppb;
+        const unsigned blocks = (unsigned)((a.seq + ppb - 1) / ppb);
+        const size_t lds = (size_t)(ppb * half) * sizeof(float2);
+        if (a.mode == 0) rope_reg_kernel<DT, 0><<<blocks, 256, lds, s>>>(a);
+        else rope_reg_kernel<DT, 1><<<blocks, 256, lds, s>>>(a);
+        return check_launch("rope");
+    }
     // ~4096 elements of work per block, bounded by the LDS table
     int64_t ppb = slab >= 4096 ? 1 : 4096 / slab;
     if (ppb * half > kRopeLds) ppb = kRopeLds / half;
     if (ppb < 1) ppb = 1;
     a.ppb = (int)ppb;
     const unsigned blocks = (unsigned)((a.seq + ppb - 1) / ppb);
-    const bool vec = aligned16(a.in) && aligned16(a.out) && slab % N == 0 &&
-                     (a.mode == 0 ? (a.dim % N == 0) : (half % N == 0));
     const size_t lds = (size_t)(ppb * half) * sizeof(float2);
     if (vec) rope_kernel<DT><<<blocks, 256, lds, s>>>(a);
     else rope_scalar_kernel<DT><<<blocks, 256, lds, s>>>(a);
