@@ -229,7 +229,7 @@ def cpu_baseline():
         O.rmsnorm(hid, g, 1e-5, O.BF16)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 200:
+        if el > 10.0:
             break
     gbs = 8 * rows * h * reps / el / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
@@ -264,12 +264,56 @@ def profile_dominant(torch, be, puter, launches):
         f"({8 * n} B algorithmic each), {launches} x 1 GiB copy")
 
 
+def measure_traffic():
+    """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
+    passes (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) over
+    `bench.py --profile-dominant 3`, each scaled by what the same counter reads
+    for the 1 GiB calibration copy in that run.  Returns (bytes, detail) or
+    (None, reason)."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    if not shutil.which("rocprofv3"):
+        return None, "rocprofv3 not found"
+    gib_kib = float(1 << 20)
+    got = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory() as tmp:
+            cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv",
+                   "-d", tmp, "-o", "run", "--", sys.executable, os.path.abspath(__file__),
+                   "--profile-dominant", "3"]
+            r = subprocess.run(cmd, capture_output=True, text=True)
+            files = [os.path.join(dp, f) for dp, _, fs in os.walk(tmp) for f in fs
+                     if f.endswith("counter_collection.csv")]
+            if not files:
+                return None, f"{counter} pass failed (rc {r.returncode})"
+            kern, copy = [], []
+            for row in csv.DictReader(open(files[0])):
+                if row.get("Counter_Name") != counter:
+                    continue
+                if "norm_wave_kernel" in row["Kernel_Name"]:
+                    kern.append(float(row["Counter_Value"]))
+                elif "copyBuffer" in row["Kernel_Name"]:
+                    copy.append(float(row["Counter_Value"]))
+            if not kern or not copy:
+                return None, f"{counter}: kernel or calibration copy missing"
+            k_kib = sum(kern) / len(kern)
+            c_kib = sum(copy) / len(copy)
+            got[counter] = (k_kib, gib_kib / c_kib)
+    fetch = got["FETCH_SIZE"][0] * got["FETCH_SIZE"][1] * 1024
+    write = got["WRITE_SIZE"][0] * got["WRITE_SIZE"][1] * 1024
+    detail = {"fetch_kib": round(got["FETCH_SIZE"][0], 1), "fetch_factor": round(got["FETCH_SIZE"][1], 4),
+              "write_kib": round(got["WRITE_SIZE"][0], 1), "write_factor": round(got["WRITE_SIZE"][1], 4)}
+    return int(fetch + write), detail
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="norm,rope,prefill,decode,cpu")
+    ap.add_argument("--only", default="norm,rope,prefill,decode,cpu,traffic")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant kernel N times plus a 1 GiB calibration copy")
     args = ap.parse_args()
@@ -305,6 +349,11 @@ def main():
         configs.update(decode(torch, be, puter, True))
         log("decode done")
     cpu = cpu_baseline() if "cpu" in only else None
+    if "traffic" in only:
+        traffic, detail = measure_traffic()
+        roof["traffic"] = traffic
+        roof["traffic_detail"] = detail
+        log(f"traffic: {traffic} B/launch ({detail})")
     value = step_bytes / (ms * 1e-3) / 1e9
     line = {
         "metric": "HBM GB/s for norm/RoPE/act; attention TFLOP/s; % of MI355X roofline",

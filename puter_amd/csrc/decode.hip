@@ -4,22 +4,34 @@
 // Reference path: KVPageGather of K and V through the sequence's page table
 // (execution/page_intrinsic.go:217-352, device/cpu/shape/page_generic.go:45-63)
 // followed by MultiHeadAttention with seqQ = 1 (bind_router.go:640-684,
-// device/cpu/attention/typed_compute.go:142-237).  Here the gather is fused:
-// the kernel reads K/V rows straight from the page pools (no materialised
-// [ctx, Hkv*D] copies), so HBM traffic is the KV bytes read once.
+// device/cpu/attention/typed_compute.go:142-237).  The gather is fused: K/V
+// rows are read straight from the page pools (no materialised [ctx, Hkv*D]
+// copies), so HBM traffic is the KV bytes read once.
 //
-// Split-K ("flash decoding"): grid = (splits of kSplit tokens, kv head, batch).
-// In a block, a group of LPT lanes owns one token (LPT x 16 B = the token's
-// D-element K row of this kv head), so every group load is one contiguous
-// 256 B (bf16) / 128 B (fp8) burst.  Each group keeps an online softmax for
-// the G = Hq/Hkv query heads that share the kv head; groups merge through
-// shuffles and LDS, and the block writes (m, l, o[D]) per query head.  A
-// second kernel merges the splits by log-sum-exp and writes bf16.
+// Split-K ("flash decoding"): grid = (kv head, 256-token splits, batch), the kv
+// head fastest so the blocks reading the 8 head slices of the same pages run
+// together; each of a block's 4 waves owns 64 consecutive tokens.  (An MFMA
+// version of the value product, V^T transposed through LDS, measured slower
+// for bf16: its LDS tile halves the blocks per CU of this memory-bound kernel.)
+//   scores: S^T[token, head] = K . Q^T with v_mfma_f32_16x16x32_bf16 (A = 16
+//     tokens x 32 dims loaded straight from the page pool into registers, B =
+//     the G query heads of the kv group, zero-padded to 16 columns); a lane then
+//     holds 16 scores of one head, so the softmax over the wave's 64 tokens is
+//     an in-lane reduction plus two shuffles - no per-token rescaling.
+//   values: O[head, d] += p[head, token] * V[token, d] on the VALU: lane owns 8
+//     dims of every 4th token (16-byte V loads), reads the token's G
+//     probabilities from a per-wave LDS row, and accumulates G x 8 sums.
+// The 16 (wave, token group) partials merge through LDS into one (m, l, o[D])
+// per query head; decode_combine_kernel merges the splits by log-sum-exp.
 #include "common.hpp"
 
 namespace puter {
 
-constexpr int kSplit = 256;   // tokens per split
+constexpr int kSplit = 256;  // tokens per split (4 waves x 64)
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 struct DecodeArgs {
     const uint16_t *q;
@@ -32,138 +44,170 @@ struct DecodeArgs {
     float scale;
 };
 
-template <int DT, int G>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
-#pragma clang fp contract(off)
-    constexpr int D = 128;
-    constexpr int ES = DT == PUTER_BF16 ? 2 : 1;
-    constexpr int EPL = 16 / ES;              // elements per lane
-    constexpr int LPT = D / EPL;              // lanes per token: 16 (bf16) / 8 (fp8)
-    constexpr int TPW = 64 / LPT;             // tokens per wave step
-    constexpr int TPB = TPW * 4;              // tokens per block step
-    constexpr int STEPS = kSplit / TPB;
-    __shared__ float red_m[4][G], red_l[4][G];
-    __shared__ float red_o[4][G][D];
+// 8 consecutive KV elements of one row as bf16.  fp8-E4M3 is widened with the
+// hardware v_cvt_pk_f32_fp8 (OCP E4M3FN on gfx950: exact for every code; every
+// E4M3 value is also a bf16 value, so the narrowing to bf16 is exact too).
+template <int KV>
+__device__ __forceinline__ uint4 load8_as_bf16(const void *pool, size_t elem_off) {
+    if constexpr (KV == PUTER_BF16) {
+        return ld_stream(reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(pool) + elem_off));
+    } else {
+        const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(pool) + elem_off);
+        const uint32_t w[2] = {raw.x, raw.y};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);  // bytes 0, 1
+            const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);   // bytes 2, 3
+            const bf16x2_t h0 = {(__bf16)f0[0], (__bf16)f0[1]};
+            const bf16x2_t h1 = {(__bf16)f1[0], (__bf16)f1[1]};
+            o[2 * k] = __builtin_bit_cast(uint32_t, h0);
+            o[2 * k + 1] = __builtin_bit_cast(uint32_t, h1);
+        }
+        return make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
 
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+template <int KV, int G>
+__global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
+    constexpr int D = 128;
+    __shared__ float p_lds[4][64][G];          // per wave: probabilities [token][head]
+    __shared__ float red_m[4][G], red_l[4][G];
+    __shared__ float red_o[4][4][G][D];        // [wave][token group][head][d]
+
+    const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
     const int ctx = (int)min((int64_t)a.ctx[b], a.max_context);
     const int t0 = split * kSplit;
     if (t0 >= ctx) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int grp = lane / LPT, sub = lane % LPT;
+    const int l16 = lane & 15, grp = lane >> 4;
     const int64_t inner = a.kv_heads * D;
-
-    // query slice: G heads x EPL dims (this lane's dims sub*EPL ..)
-    float q[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const uint16_t *qh = a.q + ((int64_t)b * a.heads + (int64_t)kvh * G + g) * D + sub * EPL;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) q[g][i] = bf16_to_f32(qh[i]);
-    }
-    const float kscale = DT == PUTER_BF16 ? 1.0f : a.ks[kvh];
     const int32_t *table = a.table + (int64_t)b * a.max_pages;
+    const int tw0 = t0 + wave * 64;
 
-    float m[G], l[G], acc[G][EPL];
+    // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero
+    bf16x8_t qb[4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) acc[g][i] = 0.0f;
-    }
-
-#pragma unroll 2
-    for (int step = 0; step < STEPS; ++step) {
-        const int t = t0 + step * TPB + wave * TPW + grp;
-        if (t0 + step * TPB >= ctx) break;
-        const bool valid = t < ctx;
-        uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-        const int32_t page = valid ? table[t / a.page_size] : -1;
-        const bool live = valid && page >= 0 && page < a.num_pages;  // bad ids read nothing
-        if (live) {
-            const int64_t row = (int64_t)page * a.page_size + t % a.page_size;
-            const size_t off = (size_t)(row * inner + (int64_t)kvh * D) * ES + sub * 16;
-            kv = ld_stream(reinterpret_cast<const uint4 *>(static_cast<const char *>(a.kp) + off));
-            vv = ld_stream(reinterpret_cast<const uint4 *>(static_cast<const char *>(a.vp) + off));
-        }
-        float kf[EPL], vf[EPL];
-        unpack_vec<DT>(kv, kf);
-        unpack_vec<DT>(vv, vf);
-        float s[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float d = 0.0f;
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) d += q[g][i] * kf[i];
-#pragma unroll
-            for (int off = LPT / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off, 64);
-            if constexpr (DT == PUTER_BF16) s[g] = round_reduction<PUTER_BF16>(d) * a.scale;
-            else s[g] = d * kscale * a.scale;
-            if (!live) s[g] = -INFINITY;
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mn = fmaxf(m[g], s[g]);
-            const float alpha = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
-            const float p = s[g] == -INFINITY ? 0.0f : __expf(s[g] - mn);
-            l[g] = l[g] * alpha + p;
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) acc[g][i] = acc[g][i] * alpha + p * vf[i];
-            m[g] = mn;
-        }
+    for (int t = 0; t < 4; ++t) {
+        uint4 u = make_uint4(0, 0, 0, 0);
+        if (l16 < G)
+            u = *reinterpret_cast<const uint4 *>(a.q + ((int64_t)b * a.heads + (int64_t)kvh * G + l16) * D + 32 * t + 8 * grp);
+        qb[t] = __builtin_bit_cast(bf16x8_t, u);
     }
 
-    // merge the TPW token groups of the wave (lanes differing in the group bits)
+    // K rows for the wave's 4 tiles of 16 tokens (A operand: token l16, dims 32t + 8grp)
+    auto row_of = [&](int tok, bool &live) -> int64_t {
+        live = tok < ctx;
+        const int32_t page = live ? table[tok / a.page_size] : 0;
+        live = live && page >= 0 && page < a.num_pages;   // bad ids are masked, never read
+        return live ? ((int64_t)page * a.page_size + tok % a.page_size) * inner + (int64_t)kvh * D : 0;
+    };
+    f32x4_t s[4];
+    bool klive[4];
 #pragma unroll
-    for (int off = LPT; off < 64; off <<= 1) {
+    for (int i = 0; i < 4; ++i) {
+        const int64_t off = row_of(tw0 + 16 * i + l16, klive[i]);
+        s[i] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mo = __shfl_xor(m[g], off, 64);
-            const float lo = __shfl_xor(l[g], off, 64);
-            const float mn = fmaxf(m[g], mo);
-            const float fa = m[g] == -INFINITY ? 0.0f : __expf(m[g] - mn);
-            const float fb = mo == -INFINITY ? 0.0f : __expf(mo - mn);
-            l[g] = l[g] * fa + lo * fb;
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) {
-                const float ao = __shfl_xor(acc[g][i], off, 64);
-                acc[g][i] = acc[g][i] * fa + ao * fb;
-            }
-            m[g] = mn;
+        for (int t = 0; t < 4; ++t) {
+            const uint4 kv = load8_as_bf16<KV>(a.kp, (size_t)(off + 32 * t + 8 * grp));
+            s[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], s[i], 0, 0, 0);
         }
     }
-    if (grp == 0) {
+    // V rows this lane accumulates: tokens tw0 + 4k + grp, dims 8*l16 .. +7
+    uint4 vv[16];
+    bool vlive[16];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            if (sub == 0) { red_m[wave][g] = m[g]; red_l[wave][g] = l[g]; }
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) red_o[wave][g][sub * EPL + i] = acc[g][i];
-        }
+    for (int k = 0; k < 16; ++k) {
+        const int64_t off = row_of(tw0 + 4 * k + grp, vlive[k]);
+        const uint4 v = load8_as_bf16<KV>(a.vp, (size_t)(off + 8 * l16));
+        vv[k] = vlive[k] ? v : make_uint4(0, 0, 0, 0);   // masked rows contribute exact zeros
     }
+
+    // softmax over the wave's 64 tokens; lane's scores: head l16, tokens 16i + 4grp + r
+    const float kscale = KV == PUTER_BF16 ? 1.0f : a.ks[kvh];
+    const float c = a.scale * kscale * 1.4426950408889634f;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = tw0 + 16 * i + 4 * grp + r;
+            float v = s[i][r];
+            if constexpr (KV == PUTER_BF16) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
+            // liveness of this token: the tile's K row owner is lane (4grp + r) of the 16
+            const bool live = __shfl(klive[i] ? 1 : 0, 4 * grp + r, 16) != 0 && tok < ctx;
+            v = live ? v * c : -INFINITY;
+            s[i][r] = v;
+            mx = fmaxf(mx, v);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mref = mx == -INFINITY ? 0.0f : mx;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float p = s[i][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i][r] - mref);
+            lsum += p;
+            if (l16 < G) p_lds[wave][16 * i + 4 * grp + r][l16] = p;
+        }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+    // O partial for token group grp: acc[h][j] = sum_k p[h][4k+grp] * V[4k+grp][8 l16 + j]
+    float acc[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        float v[8];
+        unpack_vec<PUTER_BF16>(vv[k], v);
+        float p[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) p[h] = p_lds[wave][4 * k + grp][h];
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(p[h], v[j], acc[h][j]);
+    }
+    if (lane < G) {  // lanes 0..G-1 hold head l16 = lane with grp 0
+        red_m[wave][lane] = mx;
+        red_l[wave][lane] = lsum;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red_o[wave][grp][h][8 * l16 + j] = acc[h][j];
     __syncthreads();
-    // 4 waves -> one partial per query head; thread layout: g = tid / D, d = tid % D
+
+    // merge 4 waves x 4 token groups -> one partial per query head
     for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        const int g = idx / D, d = idx % D;
+        const int h = idx / D, d = idx % D;
         float M = -INFINITY;
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][g]);
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][h]);
         float L = 0.0f, O = 0.0f;
         for (int w = 0; w < 4; ++w) {
-            const float f = red_m[w][g] == -INFINITY ? 0.0f : __expf(red_m[w][g] - M);
-            L += red_l[w][g] * f;
-            O += red_o[w][g][d] * f;
+            const float f = red_m[w][h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][h] - M);
+            L += red_l[w][h] * f;
+            O += (red_o[w][0][h][d] + red_o[w][1][h][d] + red_o[w][2][h][d] + red_o[w][3][h][d]) * f;
         }
-        const int64_t h = (int64_t)kvh * G + g;
-        const int64_t slot = ((int64_t)b * a.heads + h) * a.max_splits + split;
+        const int64_t slot = ((int64_t)b * a.heads + (int64_t)kvh * G + h) * a.max_splits + split;
         a.part_o[slot * D + d] = O;
         if (d == 0) {
-            a.part_ml[slot * 2] = M;
+            a.part_ml[slot * 2] = M;   // log2-domain max of the scaled scores
             a.part_ml[slot * 2 + 1] = L;
         }
     }
 }
 
-template <int DT>
+template <int KV>
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
     constexpr int D = 128;
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
@@ -175,12 +219,12 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
     float L = 0.0f, O = 0.0f;
     for (int s = 0; s < nsplit; ++s) {
         const float ms = a.part_ml[(base + s) * 2];
-        const float f = ms == -INFINITY ? 0.0f : __expf(ms - M);
+        const float f = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
         L += a.part_ml[(base + s) * 2 + 1] * f;
         O += a.part_o[(base + s) * D + d] * f;
     }
     float r = L > 0.0f ? O / L : 0.0f;
-    if constexpr (DT != PUTER_BF16) r *= a.vs[h / (a.heads / a.kv_heads)];
+    if constexpr (KV != PUTER_BF16) r *= a.vs[h / (a.heads / a.kv_heads)];
     a.out[((int64_t)b * a.heads + h) * D + d] = (uint16_t)f32_to_bf16(r);
 }
 
@@ -220,10 +264,12 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     if (!query || !key_pages || !value_pages || !page_table || !context_lens || !output || !workspace)
         return fail(PUTER_ERR_NIL, "paged decode: nil buffer");
     if (kv_dtype == PUTER_F8E4M3 && (!k_scale || !v_scale)) return fail(PUTER_ERR_NIL, "paged decode: fp8 needs scales");
+    if (!aligned16(query) || !aligned16(key_pages) || !aligned16(value_pages))
+        return fail(PUTER_ERR_INVALID, "paged decode: query and pools must be 16-byte aligned");
     const size_t need = puter_hip_paged_decode_workspace_bytes(batch, num_heads, head_dim, max_context);
     if (workspace_bytes < need) return fail(PUTER_ERR_INVALID, "paged decode: workspace %zu < %zu bytes", workspace_bytes, need);
     const int64_t splits = splits_for(max_context);
-    if (splits > 0x7FFFFFFF || batch > 65535 || kv_heads > 65535) return fail(PUTER_ERR_INVALID, "paged decode: grid too large");
+    if (splits > 65535 || batch > 65535 || kv_heads > 0x7FFFFFFF) return fail(PUTER_ERR_INVALID, "paged decode: grid too large");
     float *ws = static_cast<float *>(workspace);
     const int64_t slots = batch * num_heads * splits;
     DecodeArgs a{static_cast<const uint16_t *>(query), key_pages, value_pages, page_table, context_lens,
@@ -231,15 +277,15 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
                  batch, max_pages_per_seq, page_size, num_pages, num_heads, kv_heads, splits,
                  max_context, (float)(1.0 / sqrt((double)head_dim))};
     hipStream_t s = as_stream(stream);
-    const dim3 grid((unsigned)splits, (unsigned)kv_heads, (unsigned)batch);
-#define PUTER_DECODE(DT)                                                              \
+    const dim3 grid((unsigned)kv_heads, (unsigned)splits, (unsigned)batch);
+#define PUTER_DECODE(KV)                                                              \
     switch (G) {                                                                      \
-    case 1: decode_split_kernel<DT, 1><<<grid, 256, 0, s>>>(a); break;                \
-    case 2: decode_split_kernel<DT, 2><<<grid, 256, 0, s>>>(a); break;                \
-    case 4: decode_split_kernel<DT, 4><<<grid, 256, 0, s>>>(a); break;                \
-    case 8: decode_split_kernel<DT, 8><<<grid, 256, 0, s>>>(a); break;                \
+    case 1: decode_mfma_kernel<KV, 1><<<grid, 256, 0, s>>>(a); break;                 \
+    case 2: decode_mfma_kernel<KV, 2><<<grid, 256, 0, s>>>(a); break;                 \
+    case 4: decode_mfma_kernel<KV, 4><<<grid, 256, 0, s>>>(a); break;                 \
+    case 8: decode_mfma_kernel<KV, 8><<<grid, 256, 0, s>>>(a); break;                 \
     }                                                                                 \
-    decode_combine_kernel<DT><<<dim3((unsigned)num_heads, (unsigned)batch), 128, 0, s>>>(a);
+    decode_combine_kernel<KV><<<dim3((unsigned)num_heads, (unsigned)batch), 128, 0, s>>>(a);
     if (kv_dtype == PUTER_BF16) { PUTER_DECODE(PUTER_BF16) }
     else { PUTER_DECODE(PUTER_F8E4M3) }
 #undef PUTER_DECODE

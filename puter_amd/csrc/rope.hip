@@ -78,9 +78,13 @@ __global__ __launch_bounds__(256) void rope_reg_kernel(RopeArgs a) {
             }
         }
     }
+    // inverse frequencies once per pair (float64 pow), then the per-position angles
+    double *invf = reinterpret_cast<double *>(cs + a.ppb * half);
+    for (int64_t pair = tid; pair < half; pair += 256) invf[pair] = rope_inv_freq(a, pair);
+    __syncthreads();
     for (int64_t t = tid; t < np * half; t += 256) {
         const int64_t p = t / half, pair = t - p * half;
-        const double theta = (double)(p0 + p + a.start) * rope_inv_freq(a, pair);
+        const double theta = (double)(p0 + p + a.start) * invf[pair];
         double sn, cn;
         sincos(theta, &sn, &cn);
         cs[t] = make_float2((float)cn, (float)sn);
@@ -294,7 +298,7 @@ static int launch_rope(RopeArgs a, hipStream_t s) {
         if (ppb < 1) ppb = 1;
         a.ppb = (int)ppb;
         const unsigned blocks = (unsigned)((a.seq + ppb - 1) / ppb);
-        const size_t lds = (size_t)(ppb * half) * sizeof(float2);
+        const size_t lds = (size_t)(ppb * half) * sizeof(float2) + (size_t)half * sizeof(double);
         if (a.mode == 0) rope_reg_kernel<DT, 0><<<blocks, 256, lds, s>>>(a);
         else rope_reg_kernel<DT, 1><<<blocks, 256, lds, s>>>(a);
         return check_launch("rope");

@@ -93,11 +93,11 @@ def test_attention_validation(lib):
     assert lib.puter_hip_multi_head_attention(None, FAKE, FAKE, FAKE, FAKE, 8, 8, 2, None) == _lib.ERR_NIL
     # paged decode: workspace sizing and argument checks
     ws = lib.puter_hip_paged_decode_workspace_bytes(64, 32, 128, 8192)
-    assert ws == 64 * 32 * 32 * 130 * 4
+    assert ws == 64 * 32 * (8192 // 256) * 130 * 4   # 256-token splits, (m, l, o[128]) per slot
     args = [FAKE] * 5 + [2, 4, 16, 100, 32, 8, 128, 64, None, None, 2, FAKE, FAKE, ws, None]
     assert lib.puter_hip_paged_decode_attention(*args[:-4], FAKE, FAKE, 16, None) == _lib.ERR_INVALID  # workspace too small
     bad = list(args)
-    bad[10] = 64                                                    # head_dim 64 unsupported
+    bad[11] = 64                                                    # head_dim 64 unsupported
     assert lib.puter_hip_paged_decode_attention(*bad) == _lib.ERR_INVALID
     bad = list(args)
     bad[12] = 65                                                    # max_context > pages*page_size
