@@ -94,16 +94,22 @@ __device__ __forceinline__ float apply_one(float h, float mean, float inv, float
 }
 
 // ------------------------------------------------------------ fast path --
-template <int DT, int OP, bool GR, int VPL>
+// SHARE (fused gated residual + RMSNorm/LayerNorm, the block's 4 rows in one
+// modulation batch): the gate row, gamma (and beta) are staged once per block
+// in LDS instead of being re-read from L2 by every wave.
+template <int DT, int OP, bool GR, int VPL, bool SHARE = false>
 __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
 #pragma clang fp contract(off)
     constexpr int N = Vec<DT>::N;
+    constexpr int ROWV = VPL * 64;  // 16-byte vectors per row
+    extern __shared__ uint4 tbl[];  // SHARE: [gate | gamma | beta] rows
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= a.rows) return;
+    if (!SHARE && row >= a.rows) return;
+    const bool live = row < a.rows;
     const int64_t H = a.H;
-    const size_t row_vec = (size_t)row * (size_t)(H / N);
-    const int64_t batch = row / a.rows_per_batch;
+    const size_t row_vec = (size_t)(live ? row : 0) * (size_t)(H / N);
+    const int64_t batch = (live ? row : 0) / a.rows_per_batch;
 
     uint4 hv[VPL];
     if constexpr (GR) {
@@ -116,7 +122,23 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
         for (int j = 0; j < VPL; ++j) {
             rv[j] = ld_stream(res + j * 64 + lane);
             bv[j] = ld_stream(br + j * 64 + lane);
-            gv[j] = gate[j * 64 + lane];
+            if constexpr (!SHARE) gv[j] = gate[j * 64 + lane];
+        }
+        if constexpr (SHARE) {
+            // the row loads above are in flight while the block fills the table
+            const int64_t b0 = ((int64_t)blockIdx.x * 4) / a.rows_per_batch;
+            const uint4 *g0 = reinterpret_cast<const uint4 *>(a.mod) + (size_t)(b0 * a.mod_cols + a.gate_off) / N;
+            const uint4 *gm = reinterpret_cast<const uint4 *>(a.scale);
+            const uint4 *bt = reinterpret_cast<const uint4 *>(a.bias);
+            for (int i = threadIdx.x; i < ROWV; i += 256) {
+                tbl[i] = g0[i];
+                tbl[ROWV + i] = gm[i];
+                if constexpr (OP == OP_LN) tbl[2 * ROWV + i] = bt[i];
+            }
+            __syncthreads();
+            if (!live) return;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) gv[j] = tbl[j * 64 + lane];
         }
         uint4 *hid = reinterpret_cast<uint4 *>(a.hidden) + row_vec;
 #pragma unroll
@@ -173,7 +195,10 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
 
     const uint4 *gp;
     const uint4 *bp = nullptr;
-    if constexpr (OP == OP_RMS || OP == OP_LN) {
+    if constexpr (SHARE) {
+        gp = tbl + ROWV;
+        if constexpr (OP == OP_LN) bp = tbl + 2 * ROWV;
+    } else if constexpr (OP == OP_RMS || OP == OP_LN) {
         gp = reinterpret_cast<const uint4 *>(a.scale);
         if constexpr (OP == OP_LN) bp = reinterpret_cast<const uint4 *>(a.bias);
     } else {
@@ -299,6 +324,18 @@ static int launch_norm(const NormArgs &a, hipStream_t s, bool vec_ok) {
     if (vec_ok && a.H % (64 * N) == 0) {
         const int64_t vpl = a.H / (64 * N);
         const unsigned blocks = (unsigned)((a.rows + 3) / 4);
+        if constexpr (GR && (OP == OP_RMS || OP == OP_LN)) {
+            if (a.rows_per_batch % 4 == 0) {   // a block's 4 rows share one gate row
+                const size_t lds = (size_t)a.H * sizeof(typename Elem<DT>::T) * (OP == OP_LN ? 3 : 2);
+                switch (vpl) {
+                case 2: norm_wave_kernel<DT, OP, GR, 2, true><<<blocks, 256, lds, s>>>(a); return check_launch("norm");
+                case 4: norm_wave_kernel<DT, OP, GR, 4, true><<<blocks, 256, lds, s>>>(a); return check_launch("norm");
+                case 8: norm_wave_kernel<DT, OP, GR, 8, true><<<blocks, 256, lds, s>>>(a); return check_launch("norm");
+                case 16: norm_wave_kernel<DT, OP, GR, 16, true><<<blocks, 256, lds, s>>>(a); return check_launch("norm");
+                default: break;
+                }
+            }
+        }
         switch (vpl) {
         case 2: norm_wave_kernel<DT, OP, GR, 2><<<blocks, 256, 0, s>>>(a); return check_launch("norm");
         case 4: norm_wave_kernel<DT, OP, GR, 4><<<blocks, 256, 0, s>>>(a); return check_launch("norm");
