@@ -40,7 +40,8 @@ __device__ __forceinline__ double rope_inv_freq(const RopeArgs &a, int64_t pair)
 }
 
 constexpr int kRopeLds = 8192;  // max (cos, sin) entries per block (64 KiB of LDS)
-constexpr int kRopeVpt = 8;     // 16-byte vectors per thread in the register-resident kernel
+constexpr int kRopeVpt = 4;     // 16-byte vectors per thread in the register-resident kernel
+                                // (4 measured faster than 2 or 8 on the Q/K config)
 
 // Register-resident variant (a block's slab <= 256 * kRopeVpt vectors): every
 // thread issues its loads first, so the float64 angle table is computed while
