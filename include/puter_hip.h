@@ -241,6 +241,29 @@ PUTER_API int puter_hip_multi_head_attention_batched(const puter_mha_config *con
                                            int64_t batch, int64_t seq_q, int64_t seq_k,
                                            int dtype, void *stream);
 
+/* FlashAttentionConfig, device/config.go:278-281. */
+typedef struct puter_flash_config {
+    int64_t block_size; /* .BlockSize (accepted and unused, as in device/cpu/attention) */
+    int32_t causal;     /* .Causal (top-left aligned: key k > query row masked) */
+    int32_t pad_;
+} puter_flash_config;
+
+/* ScaledDotProductAttention(config, q, k, v, out, seqQ, seqK, depth, valueDim, format)
+ * interface.go:104-109: one head, Q [seqQ, depth], K [seqK, depth], V [seqK, valueDim],
+ * O [seqQ, valueDim]; online softmax through FastExp32 (cpu/attention/typed_compute.go:31-97).
+ * depth <= 8192, valueDim <= 1024 (beyond: PUTER_ERR_INVALID). */
+PUTER_API int puter_hip_scaled_dot_product_attention(const puter_flash_config *config,
+                                           const void *query, const void *key, const void *value,
+                                           void *output, int64_t seq_q, int64_t seq_k,
+                                           int64_t depth, int64_t value_dim, int dtype,
+                                           void *stream);
+/* FlashAttention(...) interface.go:92-97: the same computation
+ * (cpu/attention/ops.go:21-31 forwards to ScaledDotProductAttention). */
+PUTER_API int puter_hip_flash_attention(const puter_flash_config *config, const void *query,
+                                        const void *key, const void *value, void *output,
+                                        int64_t seq_q, int64_t seq_k, int64_t depth,
+                                        int64_t value_dim, int dtype, void *stream);
+
 /* Paged decode (extension: the reference runs KVPageGather then
  * MultiHeadAttention with seqQ = 1, page_intrinsic.go:217-352 + bind_router.go:640-684).
  * query/output [batch, Hq*D] bf16; K/V pools [pages, page_size, Hkv, D] of

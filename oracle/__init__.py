@@ -67,6 +67,8 @@ def lib():
         _lib.or_mha.argtypes = [C.POINTER(MHAConfig)] + [C.c_void_p] * 4 + [C.c_int64, C.c_int64, C.c_int]
         _lib.or_mha_rows.argtypes = ([C.POINTER(MHAConfig)] + [C.c_void_p] * 4 +
                                      [C.c_int64] * 6 + [C.c_int])
+        _lib.or_flash_attention.argtypes = ([C.c_int] + [C.c_void_p] * 4 + [C.c_int64] * 4 +
+                                            [C.c_int])
         _lib.or_paged_decode.argtypes = ([C.c_void_p] * 5 + [C.c_int64] * 6 +
                                          [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p])
         _lib.or_matmul_f32.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 3
@@ -264,6 +266,18 @@ def mha_rows(q, k, v, num_heads, head_dim, heads, rows, causal=True, kv_heads=0,
         out = np.zeros_like(q)
     _check(lib().or_mha_rows(C.byref(cfg), _p(q), _p(k), _p(v), _p(out), seq_q, seq_k,
                              heads[0], heads[1], rows[0], rows[1], dtype), "mha_rows")
+    return out
+
+
+def flash_attention(q, k, v, causal=True, dtype=F32):
+    """ScaledDotProductAttention / FlashAttention on one head: q [seqQ, depth],
+    k [seqK, depth], v [seqK, valueDim] -> [seqQ, valueDim]."""
+    q = _c(q, STORAGE[dtype]); k = _c(k, STORAGE[dtype]); v = _c(v, STORAGE[dtype])
+    seq_q, depth = q.shape
+    seq_k, value_dim = v.shape
+    out = np.zeros((seq_q, value_dim), STORAGE[dtype])
+    _check(lib().or_flash_attention(int(causal), _p(q), _p(k), _p(v), _p(out), seq_q, seq_k,
+                                    depth, value_dim, dtype), "flash_attention")
     return out
 
 

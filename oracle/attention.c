@@ -161,3 +161,59 @@ int or_paged_decode(const void *query, const void *key_pages, const void *value_
     }
     return 0;
 }
+
+/* flashExpFloat32, device/cpu/attention/flash_attention.go:171-189: -inf or
+ * anything below -88 is 0, +inf stays +inf, otherwise Activation.Exp, whose
+ * generic f32 kernel is math.FastExp32 (activation/f32_generic.go:9-16). */
+static float flash_exp(float v) {
+    if (isinf(v) && v < 0) return 0.0f;
+    if (v < -88.0f) return 0.0f;
+    if (isinf(v)) return INFINITY;
+    return or_fast_exp32(v);
+}
+
+/* ScaledDotProductAttention / FlashAttention (single head), restating
+ * device/cpu/attention/compute.go:10-29,54-68 (dispatch: zero seqQ or seqK is a
+ * no-op; scale = float32(1/sqrt(float64(depth)))) and the per-row online
+ * softmax of typed_compute.go:31-97 (16-bit dtypes) and
+ * select_flash_amd64.go:133-177 (f32): for every visible key in order
+ * (causal hides key > row, top-left aligned), score = dot * scale (16-bit
+ * dots rounded to the 16-bit format), running max, alpha =
+ * flashExp(oldMax - max), shifted = flashExp(score - max), normalizer =
+ * normalizer * alpha + shifted, acc[d] = acc[d] * alpha + v[d] * shifted;
+ * output acc[d] * (1 / normalizer), or zeros when the normalizer is 0.
+ * Layout: Q [seqQ, depth], K [seqK, depth], V [seqK, valueDim],
+ * O [seqQ, valueDim]. */
+int or_flash_attention(int causal, const void *query, const void *key, const void *value,
+                       void *output, int64_t seq_q, int64_t seq_k, int64_t depth,
+                       int64_t value_dim, int dtype) {
+    if (dtype != OR_F32 && dtype != OR_BF16 && dtype != OR_F16) return -6;
+    if (seq_q == 0 || seq_k == 0) return 0;
+    if (seq_q < 0 || seq_k < 0 || depth <= 0 || value_dim < 0) return -6;
+    const float scale = (float)(1.0 / sqrt((double)depth));
+    float *acc = (float *)malloc(sizeof(float) * (size_t)(value_dim > 0 ? value_dim : 1));
+    for (int64_t r = 0; r < seq_q; ++r) {
+        float mx = -INFINITY, norm = 0.0f;
+        for (int64_t d = 0; d < value_dim; ++d) acc[d] = 0.0f;
+        for (int64_t k = 0; k < seq_k; ++k) {
+            if (causal && k > r) continue;
+            float score = row_dot(query, (size_t)(r * depth), key, (size_t)(k * depth), depth, dtype) * scale;
+            float old = mx;
+            if (score > mx) mx = score;
+            float alpha = flash_exp(old - mx);
+            float shifted = flash_exp(score - mx);
+            norm = norm * alpha + shifted;
+            for (int64_t d = 0; d < value_dim; ++d)
+                acc[d] = acc[d] * alpha + or_load(value, (size_t)(k * value_dim + d), dtype) * shifted;
+        }
+        if (norm == 0) {
+            for (int64_t d = 0; d < value_dim; ++d) or_store(output, (size_t)(r * value_dim + d), 0.0f, dtype);
+            continue;
+        }
+        float inv = 1.0f / norm;
+        for (int64_t d = 0; d < value_dim; ++d)
+            or_store(output, (size_t)(r * value_dim + d), acc[d] * inv, dtype);
+    }
+    free(acc);
+    return 0;
+}

@@ -150,6 +150,13 @@ int or_paged_decode(const void *query, const void *key_pages, const void *value_
                     const float *k_scale, const float *v_scale, int kv_dtype,
                     void *output);
 
+/* ScaledDotProductAttention / FlashAttention: one head, Q/K [seq, depth],
+ * V/O [seq, value_dim], sequential online softmax through FastExp32; causal
+ * hides key > row (top-left aligned, unlike or_mha). */
+int or_flash_attention(int causal, const void *query, const void *key, const void *value,
+                       void *output, int64_t seq_q, int64_t seq_k, int64_t depth,
+                       int64_t value_dim, int dtype);
+
 /* ---- matmul.c ---- */
 int or_matmul_f32(float *out, const float *left, const float *right,
                   int64_t rows, int64_t inner, int64_t cols);

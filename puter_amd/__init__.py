@@ -7,7 +7,7 @@ paged-KV / attention / matmul path.
 """
 from .backend import (  # noqa: F401
     Backend, PuterError, RMSNormConfig, ModulatedLayerNormConfig, RoPEConfig,
-    MultiAxisRoPEConfig, MultiHeadAttentionConfig, F32, F16, BF16, F8E4M3, F8E5M2, I32,
+    MultiAxisRoPEConfig, MultiHeadAttentionConfig, FlashAttentionConfig, F32, F16, BF16, F8E4M3, F8E5M2, I32,
     RoPEModeInterleaved, RoPEModeHalf, RoPEScalingNone, RoPEScalingLlama3, dtype_of,
 )
 

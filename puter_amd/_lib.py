@@ -43,6 +43,10 @@ class MHAConfig(C.Structure):
                 ("pad2_", C.c_int32), ("kv_head_count", C.c_int64)]
 
 
+class FlashConfig(C.Structure):
+    _fields_ = [("block_size", C.c_int64), ("causal", C.c_int32), ("pad_", C.c_int32)]
+
+
 SIGNATURES = {
     "puter_hip_last_error": ([], C.c_char_p),
     "puter_hip_version": ([], i32),
@@ -76,6 +80,10 @@ SIGNATURES = {
                                        i32),
     "puter_hip_multi_head_attention_batched": ([C.POINTER(MHAConfig), vp, vp, vp, vp, i64, i64,
                                                 i64, i32, vp], i32),
+    "puter_hip_scaled_dot_product_attention": ([C.POINTER(FlashConfig), vp, vp, vp, vp, i64, i64,
+                                                i64, i64, i32, vp], i32),
+    "puter_hip_flash_attention": ([C.POINTER(FlashConfig), vp, vp, vp, vp, i64, i64, i64, i64,
+                                   i32, vp], i32),
     "puter_hip_paged_decode_workspace_bytes": ([i64, i64, i64, i64], sz),
     "puter_hip_paged_decode_attention": ([vp] * 5 + [i64] * 8 + [vp, vp, i32, vp, vp, sz, vp],
                                          i32),

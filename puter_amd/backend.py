@@ -78,6 +78,12 @@ class MultiHeadAttentionConfig:  # config.go:283-290
     KVHeadCount: int = 0
 
 
+@dataclass
+class FlashAttentionConfig:  # config.go:278-281
+    BlockSize: int = 0
+    Causal: bool = False
+
+
 def _ptr(x):
     if x is None:
         return None
@@ -288,6 +294,22 @@ class Backend:
         check(self.lib.puter_hip_multi_head_attention_batched(C.byref(c), _ptr(query), _ptr(key),
                                                               _ptr(value), _ptr(output), batch,
                                                               seqQ, seqK, format, self.stream()))
+
+    # device/interface.go:92-109 (single head; FlashAttention forwards to
+    # ScaledDotProductAttention as device/cpu/attention/ops.go:21-31 does)
+    def ScaledDotProductAttention(self, config, query, key, value, output, seqQ, seqK, depth,
+                                  valueDim, format):
+        c = _lib.FlashConfig(config.BlockSize, 1 if config.Causal else 0, 0)
+        check(self.lib.puter_hip_scaled_dot_product_attention(
+            C.byref(c), _ptr(query), _ptr(key), _ptr(value), _ptr(output), seqQ, seqK, depth,
+            valueDim, format, self.stream()))
+
+    def FlashAttention(self, config, query, key, value, output, seqQ, seqK, depth, valueDim,
+                       format):
+        c = _lib.FlashConfig(config.BlockSize, 1 if config.Causal else 0, 0)
+        check(self.lib.puter_hip_flash_attention(
+            C.byref(c), _ptr(query), _ptr(key), _ptr(value), _ptr(output), seqQ, seqK, depth,
+            valueDim, format, self.stream()))
 
     def PagedDecodeWorkspaceBytes(self, batch, numHeads, headDim, maxContext):
         return self.lib.puter_hip_paged_decode_workspace_bytes(batch, numHeads, headDim,

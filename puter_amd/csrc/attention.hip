@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {
     __syncthreads();
     // keys visible to this row form [k_lo, k_hi)
     int64_t k_hi = a.seq_k;
-    if (a.causal) k_hi = min(k_hi, qi + a.seq_k - a.seq_q + 1);
+    if (a.causal) k_hi = min(k_hi, qi + a.shift + 1);
     int64_t k_lo = 0;
     if (a.window > 0) k_lo = max(k_lo, qi - a.window + 1);
     float m = -INFINITY, l = 0.0f, acc = 0.0f;
@@ -92,7 +92,7 @@ static int run_mha(const puter_mha_config *config, const void *q, const void *k,
     if (!q || !k || !v || !o) return fail(PUTER_ERR_NIL, "mha: nil buffer");
     if (seq_q > 0x7FFFFFFF || H > 65535 || batch > 65535) return fail(PUTER_ERR_INVALID, "mha: grid too large");
     MhaArgs a{q, k, v, o, batch, seq_q, seq_k, H, kvh, D, config->causal ? 1 : 0,
-              config->window_size, config->alibi_slope, (float)(1.0 / sqrt((double)D))};
+              config->window_size, config->alibi_slope, (float)(1.0 / sqrt((double)D)), seq_k - seq_q};
     int status = PUTER_OK;
     if (launch_prefill_mfma(a, dtype, s, &status)) return status;
     const dim3 grid((unsigned)seq_q, (unsigned)H, (unsigned)batch);

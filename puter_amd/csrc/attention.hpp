@@ -14,6 +14,7 @@ struct MhaArgs {
     int64_t window;
     float alibi;
     float scale;
+    int64_t shift;  // causal: key k is visible to query row q iff k <= q + shift
 };
 
 // MFMA bf16 flash prefill (prefill.hip).  Returns true and sets *status when

@@ -238,4 +238,24 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// ------------------------------------------------------------ FastExp32 --
+// device/cpu/math/f32.go:21-46, evaluated operation by operation (no FMA):
+// clamps, z = x*log2(e), k = trunc(z) (one less below 0), f = z - k, a
+// degree-5 polynomial for 2^f, then k added to the exponent field.
+__device__ __forceinline__ float fast_exp32(float x) {
+    if (x < -87.33654f) return 0.0f;
+    if (x > 88.72283f) return 0x1p127f * (1.0f + (1.0f - 0x1p-23f));
+    const float z = __fmul_rn(x, 1.4426950408889634f);
+    int32_t k = (int32_t)z;
+    if (z < 0) k--;
+    const float f = __fsub_rn(z, (float)k);
+    float p = __fmul_rn(f, 0.00133389f);
+    p = __fmul_rn(f, __fadd_rn(0.00961812f, p));
+    p = __fmul_rn(f, __fadd_rn(0.05550410f, p));
+    p = __fmul_rn(f, __fadd_rn(0.24022650f, p));
+    p = __fmul_rn(f, __fadd_rn(0.69314718f, p));
+    p = __fadd_rn(1.0f, p);
+    return __uint_as_float(__float_as_uint(p) + ((uint32_t)k << 23));
+}
+
 }  // namespace puter

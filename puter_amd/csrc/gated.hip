@@ -12,23 +12,6 @@
 
 namespace puter {
 
-__device__ __forceinline__ float fast_exp32(float x) {
-    // device/cpu/math/f32.go:21-46
-    if (x < -87.33654f) return 0.0f;
-    if (x > 88.72283f) return 0x1p127f * (1.0f + (1.0f - 0x1p-23f));
-    const float z = __fmul_rn(x, 1.4426950408889634f);
-    int32_t k = (int32_t)z;
-    if (z < 0) k--;
-    const float f = __fsub_rn(z, (float)k);
-    float p = __fmul_rn(f, 0.00133389f);
-    p = __fmul_rn(f, __fadd_rn(0.00961812f, p));
-    p = __fmul_rn(f, __fadd_rn(0.05550410f, p));
-    p = __fmul_rn(f, __fadd_rn(0.24022650f, p));
-    p = __fmul_rn(f, __fadd_rn(0.69314718f, p));
-    p = __fadd_rn(1.0f, p);
-    return __uint_as_float(__float_as_uint(p) + ((uint32_t)k << 23));
-}
-
 __device__ __forceinline__ float sigmoid32(float v) {  // f32.go:88-95
     if (v >= 0) return __fdiv_rn(1.0f, __fadd_rn(1.0f, fast_exp32(-v)));
     const float e = fast_exp32(v);

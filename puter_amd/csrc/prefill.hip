@@ -1,7 +1,8 @@
 // MFMA flash-attention prefill: bf16 Q/K/V, f32 accumulation, bf16 output,
-// head_dim 128, GQA, optional causal mask (bottom-right aligned: key k is
-// visible to query q when k <= q + seqK - seqQ, as
-// device/cpu/attention/typed_compute.go:166-168).
+// head_dim 128, GQA, optional causal mask: key k is visible to query q when
+// k <= q + shift.  MultiHeadAttention passes shift = seqK - seqQ (bottom-right
+// aligned, device/cpu/attention/typed_compute.go:166-168);
+// ScaledDotProductAttention passes 0 (typed_compute.go:60-62).
 //
 // Work split: one 256-thread block (4 wave64s) per (128-query tile, head,
 // batch); wave w owns 32 queries.  K/V stream through LDS in 64-key tiles,
@@ -49,6 +50,7 @@ struct PrefillArgs {
     uint16_t *o;
     int batch, seq_q, seq_k, heads, kv_heads, qtiles;
     int causal, xcd_map;
+    int shift;         // causal: key k visible to query q iff k <= q + shift
     float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
     }
     const int kvh = h / (a.heads / a.kv_heads);
     const int q0 = qt * BM;
-    const int off = a.seq_k - a.seq_q;  // causal alignment
+    const int off = a.shift;  // causal alignment
     const int64_t qrs = (int64_t)a.heads * D, krs = (int64_t)a.kv_heads * D;
     const uint16_t *qbase = a.q + (int64_t)b * a.seq_q * qrs + (int64_t)h * D;
     const uint16_t *kbase = a.k + (int64_t)b * a.seq_k * krs + (int64_t)kvh * D;
@@ -273,7 +275,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
 
 bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
     if (dtype != PUTER_BF16 || m.dim != 128 || m.window > 0 || m.alibi != 0.0f) return false;
-    if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF) return false;
+    if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF)
+        return false;
     const uintptr_t mask = 15;
     if ((reinterpret_cast<uintptr_t>(m.q) | reinterpret_cast<uintptr_t>(m.k) |
          reinterpret_cast<uintptr_t>(m.v) | reinterpret_cast<uintptr_t>(m.o)) & mask)
@@ -290,6 +293,7 @@ bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status
     a.kv_heads = (int)m.kv_heads;
     a.qtiles = (int)((m.seq_q + fa::BM - 1) / fa::BM);
     a.causal = m.causal;
+    a.shift = (int)m.shift;
     const int G = a.heads / a.kv_heads;
     a.xcd_map = ((a.batch * a.kv_heads) % 8 == 0) ? 1 : 0;
     (void)G;

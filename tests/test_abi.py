@@ -115,3 +115,16 @@ def test_backend_class_requires_the_library():
     with pytest.raises(puter_amd.PuterError) as e:
         be.RMSNorm(puter_amd.RMSNormConfig(-1.0), FAKE, FAKE, FAKE, 4, 8, puter_amd.F32)
     assert e.value.status == _lib.ERR_INVALID
+
+
+def test_flash_attention_validation(lib):
+    fc = _lib.FlashConfig(0, 1, 0)
+    for fn in (lib.puter_hip_scaled_dot_product_attention, lib.puter_hip_flash_attention):
+        assert fn(None, FAKE, FAKE, FAKE, FAKE, 4, 4, 8, 8, 0, None) == _lib.ERR_NIL
+        assert fn(C.byref(fc), FAKE, FAKE, FAKE, FAKE, 4, 4, 8, 8, 3, None) == _lib.ERR_INVALID   # fp8
+        assert fn(C.byref(fc), None, None, None, None, 0, 4, 8, 8, 0, None) == _lib.OK            # seqQ 0
+        assert fn(C.byref(fc), None, None, None, None, 4, 0, 8, 8, 0, None) == _lib.OK            # seqK 0
+        assert fn(C.byref(fc), FAKE, FAKE, FAKE, FAKE, 4, 4, 0, 8, 0, None) == _lib.ERR_INVALID   # depth 0
+        assert fn(C.byref(fc), FAKE, FAKE, FAKE, FAKE, 4, 4, 8192 + 1, 8, 0, None) == _lib.ERR_INVALID
+        assert fn(C.byref(fc), FAKE, FAKE, FAKE, FAKE, 4, 4, 8, 1025, 0, None) == _lib.ERR_INVALID
+        assert fn(C.byref(fc), FAKE, None, FAKE, FAKE, 4, 4, 8, 8, 0, None) == _lib.ERR_NIL

@@ -158,6 +158,30 @@ def test_prefill_mfma_shapes(backend, b, sq, sk, h, kvh, causal):
             assert np.all(got[i][:sq - sk] == 0)
 
 
+@pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
+@pytest.mark.parametrize("sq,sk,d,vd,causal", [
+    (37, 37, 64, 64, True),
+    (20, 300, 48, 24, True),        # top-left causal with seqK > seqQ
+    (300, 20, 32, 80, True),        # later rows see every key
+    (65, 513, 128, 128, False),     # bf16 here takes the MFMA kernel
+    (200, 700, 128, 128, True),     # bf16 MFMA path, top-left causal
+    (3, 5, 1000, 1000, False),      # wide rows, four output dims per thread
+])
+def test_scaled_dot_product_attention(backend, dt, sq, sk, d, vd, causal):
+    import puter_amd
+    std = 1.0 / np.sqrt(d) if dt != O.F32 else 0.25
+    q = encode(seeded(500 + sq, (sq, d), 0.0, std), dt)
+    k = encode(seeded(501 + sk, (sk, d), 0.0, std), dt)
+    v = encode(seeded(502 + sk, (sk, vd)), dt)
+    ref = decode(O.flash_attention(q, k, v, causal=causal, dtype=dt), dt)
+    cfg = puter_amd.FlashAttentionConfig(64, causal)
+    for fn in (backend.ScaledDotProductAttention, backend.FlashAttention):
+        out = empty_dev((sq, vd), NP[dt])
+        fn(cfg, to_dev(q), to_dev(k), to_dev(v), out, sq, sk, d, vd, dt)
+        assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt],
+                     elem_tol=1e-3 if dt == O.F32 else None, what="sdpa")
+
+
 def paged_case(seed, batch, ctx_lo, ctx_hi, ps, h, kvh, d, kv_dt):
     rng = np.random.default_rng(seed)
     ctx = rng.integers(ctx_lo, ctx_hi + 1, batch).astype(np.int32)

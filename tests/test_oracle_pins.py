@@ -375,6 +375,60 @@ def test_mha_bf16_close_to_f64():
     assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 1e-2
 
 
+def _flash64(q, k, v, causal):
+    """float64 softmax attention of one head, top-left causal (key > row hidden)."""
+    sq, d = q.shape
+    sk = k.shape[0]
+    sc = (q.astype(np.float64) @ k.astype(np.float64).T) * np.float64(np.float32(1.0 / math.sqrt(d)))
+    if causal:
+        sc[np.arange(sk)[None, :] > np.arange(sq)[:, None]] = -np.inf
+    p = np.exp(sc - sc.max(1, keepdims=True))
+    return (p / p.sum(1, keepdims=True)) @ v.astype(np.float64)
+
+
+def test_flash_closed_forms():
+    s, d, vd = 6, 4, 3
+    q = np.zeros((s, d), np.float32)               # equal scores: FastExp32(0) = 1 exactly
+    k, v = seeded(11, (s, d)), seeded(12, (s, vd))
+    got = O.flash_attention(q, k, v, causal=True)
+    for i in range(s):
+        assert np.allclose(got[i], v[:i + 1].mean(0), atol=1e-6)
+    assert np.array_equal(got[0], v[0])            # row 0 sees key 0 only
+    nc = O.flash_attention(q, k, v, causal=False)
+    assert np.allclose(nc, np.broadcast_to(v.mean(0), nc.shape), atol=1e-6)
+
+
+@pytest.mark.parametrize("sq,sk,causal", [(9, 9, True), (4, 11, True), (11, 4, True), (7, 13, False)])
+def test_flash_f64_top_left_causal(sq, sk, causal):
+    d, vd = 16, 5                                  # depth != valueDim
+    q, k, v = seeded(13, (sq, d)), seeded(14, (sk, d)), seeded(15, (sk, vd))
+    got = O.flash_attention(q, k, v, causal=causal)
+    ref = _flash64(q, k, v, causal)
+    assert np.max(np.abs(got - ref)) < 1e-4 * max(1.0, np.max(np.abs(ref)))  # FastExp32 error
+    if causal and sq < sk:                         # bottom-right alignment would differ
+        sc = (q.astype(np.float64) @ k.T.astype(np.float64)) / math.sqrt(d)
+        sc[np.arange(sk)[None, :] > np.arange(sq)[:, None] + (sk - sq)] = -np.inf
+        p = np.exp(sc - sc.max(1, keepdims=True))
+        wrong = (p / p.sum(1, keepdims=True)) @ v
+        assert np.max(np.abs(got - wrong)) > 1e-2
+
+
+def test_flash_matches_single_head_mha_and_rounds_bf16_dot():
+    s, d = 12, 8
+    q, k, v = seeded(16, (s, d)), seeded(17, (s, d)), seeded(18, (s, d))
+    a = O.flash_attention(q, k, v, causal=True)
+    b = O.mha(q, k, v, 1, d, causal=True)          # independent restatement (f64 exp, 2 passes)
+    assert np.max(np.abs(a - b)) < 1e-4
+    qb, kb, vb = (O.from_f32(x, O.BF16) for x in (q, k, v))
+    got = O.to_f32(O.flash_attention(qb, kb, vb, causal=False, dtype=O.BF16), O.BF16)
+    qf, kf, vf = (O.to_f32(x, O.BF16).astype(np.float64) for x in (qb, kb, vb))
+    dots = O.to_f32(O.from_f32((qf @ kf.T).astype(np.float32), O.BF16), O.BF16)  # dot -> bf16
+    sc = dots.astype(np.float64) * np.float64(np.float32(1.0 / math.sqrt(d)))
+    p = np.exp(sc - sc.max(1, keepdims=True))
+    ref = (p / p.sum(1, keepdims=True)) @ vf
+    assert np.max(np.abs(got - ref)) < 1e-2 * np.max(np.abs(ref))
+
+
 def test_paged_decode_matches_gather_then_mha():
     rng = np.random.default_rng(3)
     ps, h, kvh, d = 4, 4, 2, 8
