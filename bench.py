@@ -211,6 +211,128 @@ def decode(torch, be, puter, fp8):
             "decode_sum_ctx": int(ctx.sum())}
 
 
+def block_f32(torch, be, puter):
+    """one pre-norm attention block in f32, batch 1, seq 128, hidden
+    512, 8 heads x 64: RMSNorm (eps 1e-6, gamma 1+N(0,.02)) -> Q/K/V projections
+    (weights N(0,.02)) -> RoPE (theta 1e4, the reference's default interleaved
+    mode) -> causal MHA -> output projection (7 launches).  A latency / parity
+    config: GPU latency per block, the same chain through the oracle on the host
+    (one thread per op call as the oracle runs it), and the normwise difference."""
+    import numpy as np
+    import oracle as O
+    S, HID, H, D = 128, 512, 8, 64
+    seed = 0x5EED0000
+    x = O.normal(seed, S * HID).reshape(S, HID)
+    g = O.normal(seed + 1, HID, 1.0, 0.02)
+    W = [O.normal(seed + 2 + i, HID * HID, 0.0, 0.02).reshape(HID, HID) for i in range(4)]
+
+    def host_chain():
+        h = O.rmsnorm(x, g, 1e-6, O.F32)
+        q, k, v = (O.matmul_f32(h, w) for w in W[:3])
+        q = O.rope(q.reshape(S, H, D)).reshape(S, HID)
+        k = O.rope(k.reshape(S, H, D)).reshape(S, HID)
+        o = O.mha(q, k, v, H, D, causal=True)
+        return O.matmul_f32(o, W[3])
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()  # noqa: E731
+    xd, gd = dev(x), dev(g)
+    wd = [dev(w) for w in W]
+    h, q, k, v, o, y = (torch.empty(S * HID, device="cuda") for _ in range(6))
+    ncfg = puter.RMSNormConfig(1e-6)
+    rcfg = puter.RoPEConfig(BaseFreq=10000.0)
+    mcfg = puter.MultiHeadAttentionConfig(H, D, True, 0, 0.0, H)
+
+    def gpu_chain():
+        be.RMSNorm(ncfg, xd, gd, h, S, HID, puter.F32)
+        be.Matmul(q, h, wd[0], S, HID, HID, puter.F32)
+        be.Matmul(k, h, wd[1], S, HID, HID, puter.F32)
+        be.Matmul(v, h, wd[2], S, HID, HID, puter.F32)
+        be.RoPE(rcfg, q, q, S, H, D, puter.F32)
+        be.RoPE(rcfg, k, k, S, H, D, puter.F32)
+        be.MultiHeadAttention(mcfg, q, k, v, o, S, S, puter.F32)
+        be.Matmul(y, o, wd[3], S, HID, HID, puter.F32)
+
+    gpu_chain()
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(S, HID)
+    t = Timer(torch).time(gpu_chain, 50)
+    O.set_threads(1)
+    ref = host_chain()
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 2.0:
+        host_chain()
+        reps += 1
+    cpu_ms = (time.perf_counter() - t0) / reps * 1e3
+    err = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+    flops = 4 * 2 * S * HID * HID + 4 * H * D * S * (S + 1) / 2
+    return {"block_f32_us": round(t * 1e3, 1), "block_f32_GFLOPs": round(flops / (t * 1e-3) / 1e9, 1),
+            "block_f32_normwise_err": err, "block_f32_cpu_us": round(cpu_ms * 1e3, 1),
+            "block_f32_cpu_cores": 1}
+
+
+def cpu_configs():
+    """The oracle on bounded samples of configs[2..4], timed on the host cores
+    (rope and casts are single-threaded in the oracle; SwiGLU, attention rows and
+    norms thread over rows)."""
+    import numpy as np
+    import oracle as O
+    cores = os.cpu_count() or 1
+    O.set_threads(cores)
+    res = {"cpu_cores": cores}
+
+    def timed(fn, budget=2.0):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > budget:
+                return el / reps
+    # configs[2]: RoPE on 512 tokens of Q and K, SwiGLU and casts on 512 x 14336
+    S = 512
+    q = O.from_f32(O.normal(21, S * 32 * 128).reshape(S, 32, 128), O.BF16)
+    k = O.from_f32(O.normal(22, S * 8 * 128).reshape(S, 8, 128), O.BF16)
+    t = timed(lambda: (O.rope(q, 500000.0, dtype=O.BF16), O.rope(k, 500000.0, dtype=O.BF16)))
+    res["cpu_rope_qk_bf16_GBs"] = round(4 * (q.size + k.size) / t / 1e9, 3)
+    gate = O.from_f32(O.normal(23, S * 14336), O.BF16)
+    up = O.from_f32(O.normal(24, S * 14336), O.BF16)
+    t = timed(lambda: O.gated_tensors(0, gate, up, O.BF16))
+    res["cpu_swiglu_bf16_GBs"] = round(6 * gate.size / t / 1e9, 3)
+    f = O.to_f32(gate, O.BF16)
+    t = timed(lambda: O.from_f32(f, O.BF16))
+    res["cpu_cast_f32_to_bf16_GBs"] = round(6 * f.size / t / 1e9, 3)
+    # configs[3]: causal prefill, batch 0, all 32 heads, the last 64 query rows
+    Sq, H, KV, D = 4096, 32, 8, 128
+    sc = 1.0 / math.sqrt(D)
+    qq = O.from_f32(O.normal(25, Sq * H * D, 0.0, sc).reshape(Sq, H * D), O.BF16)
+    kk = O.from_f32(O.normal(26, Sq * KV * D, 0.0, sc).reshape(Sq, KV * D), O.BF16)
+    vv = O.from_f32(O.normal(27, Sq * KV * D, 0.0, sc).reshape(Sq, KV * D), O.BF16)
+    rows = (Sq - 64, Sq)
+    t = timed(lambda: O.mha_rows(qq, kk, vv, H, D, (0, H), rows, kv_heads=KV, dtype=O.BF16))
+    flops = 4.0 * H * D * sum(r + 1 for r in range(*rows))
+    res["cpu_prefill_TFLOPs"] = round(flops / t / 1e12, 5)
+    res["cpu_prefill_sample"] = "batch 0, 32 heads, query rows 4032..4095"
+    # configs[4]: paged decode (bf16 pages) of 4 sequences, contexts ~ U[512, 8192]
+    rng = np.random.default_rng(0x5EED0004)
+    B, PS = 4, 16
+    ctx = rng.integers(512, 8193, B).astype(np.int32)
+    npg = (ctx + PS - 1) // PS
+    total = int(npg.sum())
+    perm = rng.permutation(total).astype(np.int32)
+    table = np.zeros((B, int(npg.max())), np.int32)
+    at = 0
+    for i in range(B):
+        table[i, :npg[i]] = perm[at:at + npg[i]]
+        at += npg[i]
+    kp = O.from_f32(O.normal(28, total * PS * KV * D), O.BF16)
+    vp = O.from_f32(O.normal(29, total * PS * KV * D), O.BF16)
+    qd = O.from_f32(O.normal(30, B * H * D).reshape(B, H * D), O.BF16)
+    t = timed(lambda: O.paged_decode(qd, kp, vp, table, ctx, PS, H, KV, D, O.BF16))
+    res["cpu_decode_bf16_GBs"] = round(int(ctx.sum()) * KV * D * 2 * 2 / t / 1e9, 3)
+    res["cpu_decode_sample"] = f"4 sequences, sum ctx {int(ctx.sum())}"
+    return res
+
+
 def cpu_baseline():
     """The oracle's fused GatedResidual+RMSNorm (bf16) on a bounded sample of
     the primary workload, threaded over rows on all host cores."""
@@ -313,7 +435,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="norm,rope,prefill,decode,cpu,traffic")
+    ap.add_argument("--only", default="norm,rope,prefill,decode,block,cpu,traffic")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant kernel N times plus a 1 GiB calibration copy")
     args = ap.parse_args()
@@ -348,7 +470,13 @@ def main():
         configs.update(decode(torch, be, puter, False))
         configs.update(decode(torch, be, puter, True))
         log("decode done")
+    if "block" in only:
+        configs.update(block_f32(torch, be, puter))
+        log(f"block f32: {configs['block_f32_us']} us, err {configs['block_f32_normwise_err']:.2e}")
     cpu = cpu_baseline() if "cpu" in only else None
+    if "cpu" in only:
+        configs.update(cpu_configs())
+        log("cpu configs done")
     if "traffic" in only:
         traffic, detail = measure_traffic()
         roof["traffic"] = traffic
