@@ -7,11 +7,21 @@
 // Work split: one 256-thread block (4 wave64s) per (128-query tile, head,
 // batch); wave w owns 32 queries; two blocks share a CU (2 waves per SIMD, so
 // one wave's softmax VALU work overlaps the other's MFMAs).  K/V stream
-// through LDS in 64-key tiles, double buffered: the next tile's loads go out
-// through buffer descriptors before the current tile is computed (rows past
-// the end of the sequence read as zero, so the loads need no clamping), and
-// one barrier per tile.  The wave index is read through readfirstlane so all
-// per-wave control flow is scalar.
+// through LDS in 64-key tiles, double buffered.  The tiles are copied
+// straight from HBM into LDS by buffer_load ... lds (no register staging, no
+// LDS write instructions): the next tile's copy is issued before the current
+// tile is computed and waited for (vmcnt) only at the tile's closing barrier.
+// The buffer descriptors' range ends with the last row of the sequence, so
+// rows past the end arrive as zeros.  The wave index is read through
+// readfirstlane so all per-wave control flow is scalar.
+//
+// LDS layouts (one 16 KB tile each, 256-byte rows, no padding): K row r keeps
+// its 16-byte chunk c at position c ^ (r % 16) and V row r at c ^ 4*(r % 4);
+// both swizzles make the fragment reads below bank-conflict free.  The V^T
+// operand is read from the row-major V tile with ds_read_b64_tr_b16: within a
+// 16-lane group, result lane i gets element i%4 of the 8 bytes addressed by
+// lane 4j + i/4 as its element j, so lanes 4j..4j+3 pointing at four 4-dim
+// runs of key row j deliver dims 0..15 of keys 0..3 transposed.
 //
 // Everything is computed transposed so the softmax needs no cross-lane
 // reductions beyond one permlane32 swap between the two half-waves:
@@ -51,14 +61,15 @@ namespace fa {
 constexpr int D = 128;        // head dim
 constexpr int BM = 128;       // queries per block (4 waves x 32)
 constexpr int BN = 64;        // keys per tile
-constexpr int KS = D + 8;     // K tile row stride in LDS (elements): 272 B rows, conflict-free b128 reads
-constexpr int VS = BN + 4;    // V^T tile row stride (elements): 136 B rows, conflict-free b64 reads
-constexpr int KTILE = BN * KS;
-constexpr int VTILE = D * VS;
-constexpr float RESCALE_SLACK = 8.0f;  // log2 headroom before O and l are rescaled
+constexpr int TILE_BYTES = BN * D * 2;  // one K or V tile in LDS: 16 KB
+constexpr float RESCALE_SLACK = 8.0f;   // log2 headroom before O and l are rescaled
 // buffer descriptor word 3 for raw (untyped, stride 0) dword access on gfx9
 constexpr int BUF_WORD3 = 0x00020000;
 }  // namespace fa
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 struct PrefillArgs {
     const uint16_t *q, *k, *v;
@@ -67,10 +78,6 @@ struct PrefillArgs {
     int causal, xcd_map;
     int shift;         // causal: key k visible to query q iff k <= q + shift
     float scale_log2;  // softmax scale * log2(e)
-};
-
-struct PrefillTile {
-    uint4 k[4], v[4];
 };
 
 struct PrefillState {
@@ -88,12 +95,16 @@ __device__ __forceinline__ float swap_halves_sum(float t) {
     return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
-// Issue the loads of K/V rows [kv0, kv0 + 64) for this head into registers.
-// The descriptors' range ends with the last row of the sequence, so rows past
-// the end read as zero (their scores are masked; P = 0 multiplies zero V).
-__device__ __forceinline__ void prefill_load_tile(const PrefillArgs &a, const uint16_t *kbase,
-                                                  const uint16_t *vbase, int kv0, const int (&koff)[4],
-                                                  const int (&voff)[4], PrefillTile &t) {
+__device__ __forceinline__ void wait_tile_copies() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's HBM -> LDS copies landed
+}
+
+// Copy K/V rows [kv0, kv0 + 64) of this head into LDS.  Wave w copies rows
+// 16*i + 4*w + lane/16 (i = 0..3): lane L fills chunk L%16 of its row with the
+// row's chunk (L%16) ^ swizzle(row) (kg / vg hold those byte offsets).
+__device__ __forceinline__ void prefill_copy_tile(const PrefillArgs &a, const uint16_t *kbase,
+                                                  const uint16_t *vbase, int kv0, const int (&kg)[4],
+                                                  const int (&vg)[4], char *kdst, char *vdst, int wave) {
     using namespace fa;
     const int rs2 = a.kv_heads * D * 2;  // K/V row stride in bytes
     const int rows = min(a.seq_k - kv0, BN);
@@ -104,50 +115,20 @@ __device__ __forceinline__ void prefill_load_tile(const PrefillArgs &a, const ui
     const __amdgpu_buffer_rsrc_t vd =
         __builtin_amdgcn_make_buffer_rsrc((void *)(vbase + base), (short)0, bytes, BUF_WORD3);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(kd, koff[i], 0, 0);
-        t.k[i] = make_uint4(x.x, x.y, x.z, x.w);
-    }
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kd, (lds_void *)(kdst + (16 * i + 4 * wave) * 256), 16, kg[i], 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(vd, voff[i], 0, 0);
-        t.v[i] = make_uint4(x.x, x.y, x.z, x.w);
-    }
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vd, (lds_void *)(vdst + (16 * i + 4 * wave) * 256), 16, vg[i], 0, 0, 0);
 }
 
-// K rows go to LDS as loaded; V is transposed into V^T rows.  Thread tid holds
-// K chunks tid + 256*i (row = chunk/16, 16-byte column = chunk%16) and V keys
-// kb*4 .. +3 of dims db*8 .. +7 (kb = tid%16, db = tid/16).
-__device__ __forceinline__ void prefill_store_tile(uint16_t *ks, uint16_t *vt, int tid, const PrefillTile &t) {
-    using namespace fa;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = tid + 256 * i;
-        *reinterpret_cast<uint4 *>(ks + (c >> 4) * KS + (c & 15) * 8) = t.k[i];
-    }
-    // transpose 4 keys x 8 dims into V^T rows: one 8-byte write per dim; the
-    // 16 lanes of a write pass differ in kb -> consecutive 8-byte slots of one row
-    const int kb = tid & 15, db = tid >> 4;
-    const uint32_t w[4][4] = {{t.v[0].x, t.v[0].y, t.v[0].z, t.v[0].w}, {t.v[1].x, t.v[1].y, t.v[1].z, t.v[1].w},
-                              {t.v[2].x, t.v[2].y, t.v[2].z, t.v[2].w}, {t.v[3].x, t.v[3].y, t.v[3].z, t.v[3].w}};
-#pragma unroll
-    for (int word = 0; word < 4; ++word) {
-        // v_perm_b32: low halves of keys (0,1) / (2,3) -> dim 2*word, high halves -> dim 2*word+1
-        const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][word], w[0][word], 0x05040100u),
-                                    __builtin_amdgcn_perm(w[3][word], w[2][word], 0x05040100u));
-        const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][word], w[0][word], 0x07060302u),
-                                    __builtin_amdgcn_perm(w[3][word], w[2][word], 0x07060302u));
-        *reinterpret_cast<uint2 *>(vt + (db * 8 + 2 * word) * VS + kb * 4) = lo;
-        *reinterpret_cast<uint2 *>(vt + (db * 8 + 2 * word + 1) * VS + kb * 4) = hi;
-    }
-}
-
-// One 64-key tile for this wave's 32 queries.  MASK applies the causal and
-// sequence-end mask (diagonal and tail tiles only).
-template <bool MASK>
-__device__ __forceinline__ void prefill_step(const PrefillArgs &a, const uint16_t *ks, const uint16_t *vt,
+// One 64-key tile for this wave's 32 queries.  masked applies the causal and
+// sequence-end mask (diagonal and tail tiles only).  ka / va: this lane's byte
+// offsets of its K fragments (per 16-dim step t) and V^T fragments (per
+// 32-dim block d) inside a tile.
+__device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *ks, const char *vs,
                                              const bf16x8 (&qf)[8], PrefillState &st, int qi, int kv0,
-                                             int l32, int g) {
+                                             const int (&ka)[8], const int (&va)[4], int g, bool masked) {
     using namespace fa;
     // S^T chunks: keys kv0 + 32c + (8*(r/4) + 4g + r%4), query qi; two
     // independent accumulation chains interleaved
@@ -156,18 +137,19 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const uint16_
     for (int t = 0; t < 8; ++t)
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + (32 * c + l32) * KS + 16 * t + 8 * g);
+            const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + c * 8192 + ka[t]);
             s[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], s[c], 0, 0, 0);
         }
-    if (MASK) {
+    if (masked) {
+        // key kv0 + 32c + 8(r/4) + 4g + r%4 is visible iff its offset past
+        // kv0 + 4g is <= lim (the query's last visible key, relative)
+        const int last = a.causal ? min(qi + a.shift, a.seq_k - 1) : a.seq_k - 1;
+        const int lim = last - kv0 - 4 * g;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kv0 + 32 * c + 8 * (r >> 2) + 4 * g + (r & 3);
-                const bool dead = key >= a.seq_k || (a.causal && key > qi + a.shift);
-                s[c][r] = dead ? -INFINITY : s[c][r];
-            }
+            for (int r = 0; r < 16; ++r)
+                s[c][r] = (32 * c + 8 * (r >> 2) + (r & 3)) > lim ? -INFINITY : s[c][r];
     }
     float tmax = -INFINITY;
 #pragma unroll
@@ -199,25 +181,31 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const uint16_
                 pf[c][h][j] = (__bf16)p;  // v_cvt_pk_bf16_f32: round to nearest even
             }
     st.l += psum;
-    // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; four independent chains
+    // O^T[d, q] += V^T[d, keys] . P^T[keys, q]: the V^T fragment (dims 32d +
+    // lane%32, keys 32c + 16h + 4g + 0..3 and + 8) is two transposing reads
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                const uint16_t *row = vt + (32 * d + l32) * VS + 32 * c + 16 * h + 4 * g;
-                const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(row);
-                const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(row + 8);
-                const bf16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                const char *p = vs + (32 * c + 16 * h) * 256 + va[d];
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * 256));
+                const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 st.o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[c][h], st.o[d], 0, 0, 0);
             }
 }
 
 __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a) {
     using namespace fa;
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][KTILE];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][VTILE];
+    // four separate arrays (not one indexed by parity) so the compiler can
+    // tell the tile being copied from the tile being read and does not wait
+    // for the copy before the reads
+    __shared__ __attribute__((aligned(1024))) char k0s[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k1s[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v0s[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v1s[TILE_BYTES];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -271,15 +259,31 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
     if (a.causal) nfree = min(nfree, q0 + a.shift + 1 > 0 ? (q0 + a.shift + 1) / BN : 0);
     nfree = min(nfree, ntiles);
 
-    // loop-invariant byte offsets of this thread's K / V chunks inside a tile
-    int koff[4], voff[4];
+    // byte offsets of this lane's tile copies (source side, swizzled) ...
+    int kg[4], vg[4];
     {
         const int rs2 = a.kv_heads * D * 2;
+        const int pos = lane & 15;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i;
-            koff[i] = (c >> 4) * rs2 + (c & 15) * 16;
-            voff[i] = ((tid & 15) * 4 + i) * rs2 + (tid >> 4) * 16;
+            const int row = 16 * i + 4 * wave + (lane >> 4);
+            kg[i] = row * rs2 + ((pos ^ (row & 15)) << 4);
+            vg[i] = row * rs2 + ((pos ^ ((row & 3) << 2)) << 4);
+        }
+    }
+    // ... and of its fragment reads: K row l32 (+32c), chunk (2t + g) ^ (l32 % 16);
+    // V: lane group q = lane/16, i = lane%16 = 4j + m reads key row 4(q/2) + j,
+    // dims 16(q%2) + 4m .. +3 of dim block d: chunk (4d + 2(q%2) + m/2) ^ 4*(row%4), half m%2
+    int ka[8], va[4];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ka[t] = l32 * 256 + (((2 * t + g) ^ (l32 & 15)) << 4);
+    {
+        const int q = lane >> 4, i = lane & 15, j = i >> 2, m = i & 3;
+        const int row = 4 * (q >> 1) + j;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int chunk = (4 * d + 2 * (q & 1) + (m >> 1)) ^ ((row & 3) << 2);
+            va[d] = row * 256 + (chunk << 4) + 8 * (m & 1);
         }
     }
     PrefillState st;
@@ -288,33 +292,26 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
     st.m = -INFINITY;
     st.l = 0.0f;
 
-    if (ntiles > 0) {
-        PrefillTile t0;
-        prefill_load_tile(a, kbase, vbase, 0, koff, voff, t0);
-        prefill_store_tile(k_lds[0], v_lds[0], tid, t0);
-    }
+    if (ntiles > 0) prefill_copy_tile(a, kbase, vbase, 0, kg, vg, k0s, v0s, wave);
+    wait_tile_copies();
     __syncthreads();
-    // The next tile's loads are issued before the current tile is computed
-    // (the last iteration re-reads its own tile: cheaper than a branch).
-    int it = 0;
-    for (; it < nfree; ++it) {
+    // one tile: copy the next tile into the other buffers, compute this one,
+    // then wait for the copy and meet at the barrier
+    auto tile = [&](int it, const char *kc, const char *vc, char *kn, char *vn) __attribute__((always_inline)) {
         const int kv0 = it * BN;
-        PrefillTile nx;
-        prefill_load_tile(a, kbase, vbase, min(kv0 + BN, (ntiles - 1) * BN), koff, voff, nx);
-        prefill_step<false>(a, k_lds[it & 1], v_lds[it & 1], qf, st, qi, kv0, l32, g);
-        if (it + 1 < ntiles) prefill_store_tile(k_lds[(it & 1) ^ 1], v_lds[(it & 1) ^ 1], tid, nx);
-        __syncthreads();
-    }
-    for (; it < ntiles; ++it) {
-        const int kv0 = it * BN;
-        PrefillTile nx;
-        prefill_load_tile(a, kbase, vbase, min(kv0 + BN, (ntiles - 1) * BN), koff, voff, nx);
+        if (it + 1 < ntiles) prefill_copy_tile(a, kbase, vbase, kv0 + BN, kg, vg, kn, vn, wave);
         // waves whose queries all precede this tile skip it
         if (!a.causal || kv0 <= qlast + a.shift)
-            prefill_step<true>(a, k_lds[it & 1], v_lds[it & 1], qf, st, qi, kv0, l32, g);
-        if (it + 1 < ntiles) prefill_store_tile(k_lds[(it & 1) ^ 1], v_lds[(it & 1) ^ 1], tid, nx);
+            prefill_step(a, kc, vc, qf, st, qi, kv0, ka, va, g, it >= nfree);
+        wait_tile_copies();
         __syncthreads();
+    };
+    int it = 0;
+    for (; it + 1 < ntiles; it += 2) {
+        tile(it, k0s, v0s, k1s, v1s);
+        tile(it + 1, k1s, v1s, k0s, v0s);
     }
+    if (it < ntiles) tile(it, k0s, v0s, k1s, v1s);
 
     // normalise and store: lane holds O[qi][32d + 8*(r/4) + 4g + r%4]
     const float ltot = swap_halves_sum(st.l);
