@@ -42,89 +42,168 @@ __device__ __forceinline__ double rope_inv_freq(const RopeArgs &a, int64_t pair)
 constexpr int kRopeLds = 8192;  // max (cos, sin) entries per block (64 KiB of LDS)
 constexpr int kRopeVpt = 4;     // 16-byte vectors per thread in the register-resident kernel
                                 // (4 measured faster than 2 or 8 on the Q/K config)
+constexpr int kRopeGroupLds = 2048;  // (cos, sin) entries per group table in the pipelined kernel
+constexpr int kRopeMaxBlocks = 2048; // 8 blocks per CU on MI355X's 256 CUs
 
-// Register-resident variant (a block's slab <= 256 * kRopeVpt vectors): every
-// thread issues its loads first, so the float64 angle table is computed while
-// the data is in flight; then one barrier, rotate, store.  MODE 0 interleaved,
-// 1 half.
-template <int DT, int MODE>
+// Register-resident, pipelined variant (a group of a.ppb positions is at most
+// 256 * kRopeVpt vectors).  Blocks stride over the position groups; each block
+// computes the float64 inverse frequencies once, then for every group it
+// owns: issue the next group's loads and fill the next group's (cos, sin)
+// table (float64) while the current group's data is rotated and stored.  The
+// table is double buffered in LDS, the data in registers.  MODE 0
+// interleaved, 1 half.  FAST: every group is full and its items fill all
+// 256 * ITEMS slots, so the loop has no per-item branch and the group barrier
+// waits for LDS only; with no branch around any load or store the compiler
+// waits for exactly the current group's loads instead of draining every
+// outstanding access (which would also wait for the stores just issued).
+template <int DT, int MODE, bool FAST>
 __global__ __launch_bounds__(256) void rope_reg_kernel(RopeArgs a) {
 #pragma clang fp contract(off)
-    extern __shared__ float2 cs[];
-    using T = typename Elem<DT>::T;
+    extern __shared__ float2 cs[];  // [2][ppb * half] tables, then half doubles
     constexpr int N = Vec<DT>::N;
-    const int64_t half = a.dim / 2;
-    const int64_t p0 = (int64_t)blockIdx.x * a.ppb;
-    const int64_t np = min((int64_t)a.ppb, a.seq - p0);
-    const int64_t slab = a.heads * a.dim;
-    const uint4 *in = reinterpret_cast<const uint4 *>(reinterpret_cast<const T *>(a.in) + p0 * slab);
-    uint4 *out = reinterpret_cast<uint4 *>(reinterpret_cast<T *>(a.out) + p0 * slab);
-    const int tid = threadIdx.x;
-    const int64_t vhalf = half / N;
-    // MODE 0: item k = vector tid + 256k.  MODE 1: item k = (lo, hi) vector pair
-    const int64_t nitems = MODE == 0 ? np * slab / N : np * a.heads * vhalf;
     constexpr int ITEMS = MODE == 0 ? kRopeVpt : kRopeVpt / 2;
-    uint4 lo[ITEMS], hi[ITEMS];
+    // group-local sizes fit 32 bits: a group holds <= 256 * kRopeVpt vectors
+    const int half = (int)(a.dim / 2);
+    const int dim = (int)a.dim;
+    const int slab = (int)(a.heads * a.dim);
+    const int vhalf = half / N;
+    const int ppb = a.ppb;
+    const int tsize = ppb * half;
+    const int64_t ngroups = (a.seq + ppb - 1) / ppb;
+    const int tid = threadIdx.x;
+    double *invf = reinterpret_cast<double *>(cs + 2 * tsize);
+
+    // Every group has the same layout, so each item's vector offset inside the
+    // group, its table index and its position are computed once and packed
+    // into one register: offset < 1024 (10 bits), table index < 2048 (11
+    // bits), position < 1024 (10 bits).  Item k covers group vector tid + 256k
+    // (MODE 0) or the (lo, hi) pair of the k-th half-row vector (MODE 1).
+    // Quotients of operands below 2^12 come from a float reciprocal:
+    // (x + 0.5) / d is at least 0.5 / d from an integer, far more than the
+    // float rounding, so truncation gives floor(x / d) exactly.
+    auto quot = [](int x, float rcp) -> int { return (int)(((float)x + 0.5f) * rcp); };
+    const float r_slab = 1.0f / (float)slab, r_dim = 1.0f / (float)dim;
+    const float r_vhalf = 1.0f / (float)vhalf, r_heads = 1.0f / (float)a.heads;
+    uint32_t info[ITEMS];
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) {
-        const int64_t w = tid + 256 * k;
-        if (w < nitems) {
-            if constexpr (MODE == 0) {
-                lo[k] = ld_stream(in + w);
-            } else {
-                const int64_t row = w / vhalf, j = w - row * vhalf;
-                const int64_t v = row * a.dim / N + j;
-                lo[k] = ld_stream(in + v);
-                hi[k] = ld_stream(in + v + vhalf);
-            }
-        }
-    }
-    // inverse frequencies once per pair (float64 pow), then the per-position angles
-    double *invf = reinterpret_cast<double *>(cs + a.ppb * half);
-    for (int64_t pair = tid; pair < half; pair += 256) invf[pair] = rope_inv_freq(a, pair);
-    __syncthreads();
-    for (int64_t t = tid; t < np * half; t += 256) {
-        const int64_t p = t / half, pair = t - p * half;
-        const double theta = (double)(p0 + p + a.start) * invf[pair];
-        double sn, cn;
-        sincos(theta, &sn, &cn);
-        cs[t] = make_float2((float)cn, (float)sn);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < ITEMS; ++k) {
-        const int64_t w = tid + 256 * k;
-        if (w >= nitems) continue;
+        const int w = tid + 256 * k;
+        int voff, tix, p;
         if constexpr (MODE == 0) {
-            const int64_t e0 = w * N;
-            const int64_t p = e0 / slab;
-            const int64_t pair0 = (e0 - p * slab) % a.dim / 2;
-            float f[N], o[N];
-            unpack_vec<DT>(lo[k], f);
-#pragma unroll
-            for (int i = 0; i < N / 2; ++i) {
-                const float2 c = cs[p * half + pair0 + i];
-                o[2 * i] = f[2 * i] * c.x - f[2 * i + 1] * c.y;
-                o[2 * i + 1] = f[2 * i] * c.y + f[2 * i + 1] * c.x;
-            }
-            st_stream(pack_vec<DT>(o), out + w);
+            const int e0 = w * N;
+            p = quot(e0, r_slab);
+            const int in_slab = e0 - p * slab;
+            voff = w;
+            tix = p * half + (in_slab - quot(in_slab, r_dim) * dim) / 2;
         } else {
-            const int64_t row = w / vhalf, j = w - row * vhalf;
-            const int64_t p = row / a.heads;
-            const int64_t v = row * a.dim / N + j;
-            float e[N], od[N], oe[N], oo[N];
-            unpack_vec<DT>(lo[k], e);
-            unpack_vec<DT>(hi[k], od);
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-                const float2 c = cs[p * half + j * N + i];
-                oe[i] = e[i] * c.x - od[i] * c.y;
-                oo[i] = e[i] * c.y + od[i] * c.x;
-            }
-            st_stream(pack_vec<DT>(oe), out + v);
-            st_stream(pack_vec<DT>(oo), out + v + vhalf);
+            const int row = quot(w, r_vhalf), j = w - row * vhalf;
+            p = quot(row, r_heads);
+            voff = row * (dim / N) + j;
+            tix = p * half + j * N;
         }
+        if (p >= ppb) voff = tix = 0;  // inactive in every group
+        info[k] = (uint32_t)voff | ((uint32_t)tix << 10) | ((uint32_t)min(p, 1023) << 21);
     }
+    const uint4 *inv = reinterpret_cast<const uint4 *>(a.in);
+    uint4 *outv = reinterpret_cast<uint4 *>(a.out);
+    // exact: the group's items fill all 256 * ITEMS slots, so every item of a
+    // full group is live and the loads / stores need no per-item guard
+    auto live = [&](int k, int np) -> bool { return FAST || (int)(info[k] >> 21) < np; };
+    auto load = [&](int64_t g, uint4 (&lo)[ITEMS], uint4 (&hi)[ITEMS]) __attribute__((always_inline)) {
+        const int np = (int)min((int64_t)ppb, a.seq - g * ppb);
+        const uint4 *gb = inv + g * ppb * (int64_t)(slab / N);  // first vector of the group
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            if (live(k, np)) {
+                const int voff = info[k] & 1023;
+                lo[k] = ld_stream(gb + voff);
+                if constexpr (MODE == 1) hi[k] = ld_stream(gb + voff + vhalf);
+            }
+        }
+    };
+    auto table = [&](int64_t g, float2 *t) __attribute__((always_inline)) {
+        const int64_t p0 = g * ppb;
+        const int n = (int)min((int64_t)ppb, a.seq - p0) * half;
+        for (int e = tid; e < n; e += 256) {
+            const int p = e / half, pair = e - p * half;
+            const double theta = (double)(p0 + p + a.start) * invf[pair];
+            double sn, cn;
+            sincos(theta, &sn, &cn);
+            t[e] = make_float2((float)cn, (float)sn);
+        }
+    };
+
+    // rotate and store group g from registers with table c0
+    auto rotate = [&](int64_t g, const float2 *c0, const uint4 (&lo)[ITEMS], const uint4 (&hi)[ITEMS])
+                      __attribute__((always_inline)) {
+        const int np = (int)min((int64_t)ppb, a.seq - g * ppb);
+        uint4 *gb = outv + g * ppb * (int64_t)(slab / N);
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            if (!live(k, np)) continue;
+            const int voff = info[k] & 1023, tix = (info[k] >> 10) & 2047;
+            if constexpr (MODE == 0) {
+                float f[N], o[N];
+                unpack_vec<DT>(lo[k], f);
+#pragma unroll
+                for (int i = 0; i < N / 2; ++i) {
+                    const float2 c = c0[tix + i];
+                    o[2 * i] = f[2 * i] * c.x - f[2 * i + 1] * c.y;
+                    o[2 * i + 1] = f[2 * i] * c.y + f[2 * i + 1] * c.x;
+                }
+                st_stream(pack_vec<DT>(o), gb + voff);
+            } else {
+                float e[N], od[N], oe[N], oo[N];
+                unpack_vec<DT>(lo[k], e);
+                unpack_vec<DT>(hi[k], od);
+#pragma unroll
+                for (int i = 0; i < N; ++i) {
+                    const float2 c = c0[tix + i];
+                    oe[i] = e[i] * c.x - od[i] * c.y;
+                    oo[i] = e[i] * c.y + od[i] * c.x;
+                }
+                st_stream(pack_vec<DT>(oe), gb + voff);
+                st_stream(pack_vec<DT>(oo), gb + voff + vhalf);
+            }
+        }
+    };
+
+    // first group: loads go out before the float64 inverse frequencies
+    int64_t g = blockIdx.x;
+    if (g >= ngroups) return;  // block-uniform: the whole block leaves together
+    uint4 lo[ITEMS], hi[ITEMS];
+    load(g, lo, hi);
+    for (int pair = tid; pair < half; pair += 256) invf[pair] = rope_inv_freq(a, pair);
+    __syncthreads();
+    table(g, cs);
+    __syncthreads();
+    int buf = 0;
+    // every iteration of this loop has a next group, so its loads and table are
+    // issued unconditionally (no branch around them: the compiler then waits
+    // for exactly the current group's loads); the block's last group is
+    // rotated after the loop with nothing left to prefetch
+    for (; g + gridDim.x < ngroups; g += gridDim.x) {
+        const int64_t nx = g + gridDim.x;
+        uint4 nlo[ITEMS], nhi[ITEMS];
+        load(nx, nlo, nhi);
+        table(nx, cs + (buf ^ 1) * tsize);
+        rotate(g, cs + buf * tsize, lo, hi);
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            lo[k] = nlo[k];
+            hi[k] = nhi[k];
+        }
+        // next table complete; this table free for the group after next.
+        // FAST waits for LDS only (loads / stores stay in flight).
+        if (FAST) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+        } else {
+            __syncthreads();
+        }
+        buf ^= 1;
+    }
+    rotate(g, cs + buf * tsize, lo, hi);
 }
 
 template <int DT>
@@ -292,16 +371,24 @@ static int launch_rope(RopeArgs a, hipStream_t s) {
     const bool vec = aligned16(a.in) && aligned16(a.out) && slab % N == 0 &&
                      (a.mode == 0 ? (a.dim % N == 0) : (half % N == 0));
     const int64_t slab_vec = slab / N;
-    if (vec && slab_vec <= 256 * kRopeVpt) {
-        // as many positions per block as fill the registers, bounded by the table
+    if (vec && slab_vec <= 256 * kRopeVpt && half <= kRopeGroupLds) {
+        // as many positions per group as fill the registers, bounded by the table
         int64_t ppb = (256 * kRopeVpt) / slab_vec;
-        if (ppb * half > kRopeLds) ppb = kRopeLds / half;
+        if (ppb * half > kRopeGroupLds) ppb = kRopeGroupLds / half;
         if (ppb < 1) ppb = 1;
         a.ppb = (int)ppb;
-        const unsigned blocks = (unsigned)((a.seq + ppb - 1) / ppb);
-        const size_t lds = (size_t)(ppb * half) * sizeof(float2) + (size_t)half * sizeof(double);
-        if (a.mode == 0) rope_reg_kernel<DT, 0><<<blocks, 256, lds, s>>>(a);
-        else rope_reg_kernel<DT, 1><<<blocks, 256, lds, s>>>(a);
+        const int64_t groups = (a.seq + ppb - 1) / ppb;
+        const unsigned blocks = (unsigned)min(groups, (int64_t)kRopeMaxBlocks);
+        const size_t lds = 2 * (size_t)(ppb * half) * sizeof(float2) + (size_t)half * sizeof(double);
+        constexpr int items = 256 * kRopeVpt;  // vectors a group can hold
+        const bool fast = a.seq % ppb == 0 && ppb * slab_vec == items;
+        if (a.mode == 0) {
+            if (fast) rope_reg_kernel<DT, 0, true><<<blocks, 256, lds, s>>>(a);
+            else rope_reg_kernel<DT, 0, false><<<blocks, 256, lds, s>>>(a);
+        } else {
+            if (fast) rope_reg_kernel<DT, 1, true><<<blocks, 256, lds, s>>>(a);
+            else rope_reg_kernel<DT, 1, false><<<blocks, 256, lds, s>>>(a);
+        }
         return check_launch("rope");
     }
     // ~4096 elements of work per block, bounded by the LDS table
