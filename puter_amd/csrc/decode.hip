@@ -82,6 +82,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int l16 = lane & 15, grp = lane >> 4;
     const int64_t inner = a.kv_heads * D;
+    const int ps = (int)a.page_size;
     const int32_t *table = a.table + (int64_t)b * a.max_pages;
     const int tw0 = t0 + wave * 64;
 
@@ -95,18 +96,31 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         qb[t] = __builtin_bit_cast(bf16x8_t, u);
     }
 
+    // Token resolution, once per lane: lane L owns token tw0 + L and looks up
+    // its page (one coalesced read of the page-table row); the pool row index
+    // (page * page_size + slot, -1 for dead tokens and bad page ids, which are
+    // masked and never read) is then passed to the lanes that load that token
+    // by a cross-lane shuffle.
+    int myrow = -1;
+    {
+        const int tok = tw0 + lane;
+        if (tok < ctx) {
+            const int pidx = tok / ps;
+            const int32_t page = table[pidx];
+            if (page >= 0 && page < a.num_pages) myrow = page * ps + (tok - pidx * ps);
+        }
+    }
+    const int64_t head_off = (int64_t)kvh * D;
+    auto row_off = [&](int row) -> int64_t { return (int64_t)row * inner + head_off; };
+
     // K rows for the wave's 4 tiles of 16 tokens (A operand: token l16, dims 32t + 8grp)
-    auto row_of = [&](int tok, bool &live) -> int64_t {
-        live = tok < ctx;
-        const int32_t page = live ? table[tok / a.page_size] : 0;
-        live = live && page >= 0 && page < a.num_pages;   // bad ids are masked, never read
-        return live ? ((int64_t)page * a.page_size + tok % a.page_size) * inner + (int64_t)kvh * D : 0;
-    };
     f32x4_t s[4];
     bool klive[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int64_t off = row_of(tw0 + 16 * i + l16, klive[i]);
+        const int row = __shfl(myrow, 16 * i + l16, 64);
+        klive[i] = row >= 0;
+        const int64_t off = klive[i] ? row_off(row) : 0;
         s[i] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -116,12 +130,12 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     }
     // V rows this lane accumulates: tokens tw0 + 4k + grp, dims 8*l16 .. +7
     uint4 vv[16];
-    bool vlive[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        const int64_t off = row_of(tw0 + 4 * k + grp, vlive[k]);
+        const int row = __shfl(myrow, 4 * k + grp, 64);
+        const int64_t off = row >= 0 ? row_off(row) : 0;
         const uint4 v = load8_as_bf16<KV>(a.vp, (size_t)(off + 8 * l16));
-        vv[k] = vlive[k] ? v : make_uint4(0, 0, 0, 0);   // masked rows contribute exact zeros
+        vv[k] = row >= 0 ? v : make_uint4(0, 0, 0, 0);   // masked rows contribute exact zeros
     }
 
     // softmax over the wave's 64 tokens; lane's scores: head l16, tokens 16i + 4grp + r
@@ -136,7 +150,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             float v = s[i][r];
             if constexpr (KV == PUTER_BF16) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
             // liveness of this token: the tile's K row owner is lane (4grp + r) of the 16
-            const bool live = __shfl(klive[i] ? 1 : 0, 4 * grp + r, 16) != 0 && tok < ctx;
+            const bool live = __shfl(klive[i] ? 1 : 0, 4 * grp + r, 16) != 0;
             v = live ? v * c : -INFINITY;
             s[i][r] = v;
             mx = fmaxf(mx, v);
@@ -259,6 +273,8 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     const int64_t G = num_heads / kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return fail(PUTER_ERR_INVALID, "paged decode: group size %lld unsupported", (long long)G);
     if (kv_dtype != PUTER_BF16 && kv_dtype != PUTER_F8E4M3) return fail(PUTER_ERR_INVALID, "paged decode: kv dtype %d unsupported", kv_dtype);
+    if (num_pages > 0 && (num_pages > 0x7FFFFFFF / page_size || max_pages_per_seq > 0x7FFFFFFF / page_size))
+        return fail(PUTER_ERR_INVALID, "paged decode: pool rows (num_pages * page_size) must stay below 2^31");
     if (max_context <= 0 || max_context > max_pages_per_seq * page_size)
         return fail(PUTER_ERR_INVALID, "paged decode: max_context must be in [1, max_pages_per_seq*page_size]");
     if (!query || !key_pages || !value_pages || !page_table || !context_lens || !output || !workspace)
