@@ -21,8 +21,9 @@
 //   values: O[head, d] += p[head, token] * V[token, d] on the VALU: lane owns 8
 //     dims of every 4th token (16-byte V loads), reads the token's G
 //     probabilities from a per-wave LDS row, and accumulates G x 8 sums.
-// The 16 (wave, token group) partials merge through LDS into one (m, l, o[D])
-// per query head; decode_combine_kernel merges the splits by log-sum-exp.
+// A wave's 4 token-group partials are summed in registers (lane-row swaps),
+// the 4 waves' partials merge through LDS into one (m, l, o[D]) per query
+// head; decode_combine_kernel merges the splits by log-sum-exp.
 #include "common.hpp"
 
 namespace puter {
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     constexpr int D = 128;
     __shared__ float p_lds[4][64][G];          // per wave: probabilities [token][head]
     __shared__ float red_m[4][G], red_l[4][G];
-    __shared__ float red_o[4][4][G][D];        // [wave][token group][head][d]
+    __shared__ float red_o[4][G][D];           // [wave][head][d], token groups already summed
 
     const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
     const int ctx = (int)min((int64_t)a.ctx[b], a.max_context);
@@ -191,17 +192,31 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(p[h], v[j], acc[h][j]);
     }
+    // sum the 4 token groups (16-lane rows) in registers: permlane16_swap pairs
+    // rows (0,1) and (2,3), permlane32_swap then pairs the two halves, leaving
+    // the full sum in every row; row grp stores head grp % G's values
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = acc[h][j];
+            const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+            const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            acc[h][j] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+        }
     if (lane < G) {  // lanes 0..G-1 hold head l16 = lane with grp 0
         red_m[wave][lane] = mx;
         red_l[wave][lane] = lsum;
     }
 #pragma unroll
     for (int h = 0; h < G; ++h)
+        if ((h & 3) == grp)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) red_o[wave][grp][h][8 * l16 + j] = acc[h][j];
+            for (int j = 0; j < 8; ++j) red_o[wave][h][8 * l16 + j] = acc[h][j];
     __syncthreads();
 
-    // merge 4 waves x 4 token groups -> one partial per query head
+    // merge the 4 waves -> one partial per query head
     for (int idx = threadIdx.x; idx < G * D; idx += 256) {
         const int h = idx / D, d = idx % D;
         float M = -INFINITY;
@@ -210,7 +225,7 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
         for (int w = 0; w < 4; ++w) {
             const float f = red_m[w][h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][h] - M);
             L += red_l[w][h] * f;
-            O += (red_o[w][0][h][d] + red_o[w][1][h][d] + red_o[w][2][h][d] + red_o[w][3][h][d]) * f;
+            O += red_o[w][h][d] * f;
         }
         const int64_t slot = ((int64_t)b * a.heads + (int64_t)kvh * G + h) * a.max_splits + split;
         a.part_o[slot * D + d] = O;
@@ -221,6 +236,10 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
     }
 }
 
+// One (query head, sequence) per block, one output dim per thread: merge the
+// sequence's split partials by log-sum-exp.  The (m, l) pairs are read by
+// all threads (the same addresses: one transaction), the split loop is
+// unrolled 4-wide so its loads are in flight together.
 template <int KV>
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
     constexpr int D = 128;
@@ -228,14 +247,32 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
     const int ctx = (int)min((int64_t)a.ctx[b], a.max_context);
     const int nsplit = (ctx + kSplit - 1) / kSplit;
     const int64_t base = ((int64_t)b * a.heads + h) * a.max_splits;
+    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + base;
+    const float *po = a.part_o + base * D + d;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.part_ml[(base + s) * 2]);
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[s].x);
     float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-        const float ms = a.part_ml[(base + s) * 2];
-        const float f = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-        L += a.part_ml[(base + s) * 2 + 1] * f;
-        O += a.part_o[(base + s) * D + d] * f;
+    int s = 0;
+    for (; s + 4 <= nsplit; s += 4) {
+        float2 m4[4];
+        float o4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            m4[u] = ml[s + u];
+            o4[u] = po[(int64_t)(s + u) * D];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float f = m4[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m4[u].x - M);
+            L += m4[u].y * f;
+            O += o4[u] * f;
+        }
+    }
+    for (; s < nsplit; ++s) {
+        const float2 m1 = ml[s];
+        const float f = m1.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1.x - M);
+        L += m1.y * f;
+        O += po[(int64_t)s * D] * f;
     }
     float r = L > 0.0f ? O / L : 0.0f;
     if constexpr (KV != PUTER_BF16) r *= a.vs[h / (a.heads / a.kv_heads)];
