@@ -36,9 +36,11 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
-    def time(self, fn, iters):
+    def time(self, fn, iters, warmup=0):
         t = self.torch
         s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        for _ in range(warmup):
+            fn()
         t.cuda.synchronize()
         s.record()
         for _ in range(iters):
@@ -157,7 +159,7 @@ def prefill(torch, be, puter):
     cfg = puter.MultiHeadAttentionConfig(H, D, True, 0, 0.0, KV)
     fn = lambda: be.MultiHeadAttentionBatched(cfg, q, k, v, o, B, S, S, puter.BF16)  # noqa: E731
     fn()
-    t = Timer(torch).time(fn, 5)
+    t = Timer(torch).time(fn, 10, warmup=3)
     flops = 4.0 * B * H * D * S * (S + 1) / 2
     tf = flops / (t * 1e-3) / 1e12
     return {"prefill_ms": round(t, 3), "prefill_TFLOPs": round(tf, 1),
@@ -202,7 +204,7 @@ def decode(torch, be, puter, fp8):
     fn = lambda: be.PagedDecodeAttention(q, kp, vp, tt, cc, B, maxp, PS, total, H, KV, D, maxc, ks, vs, fmt,  # noqa: E731
                                          out, ws, wsb)
     fn()
-    t = Timer(torch).time(fn, 20)
+    t = Timer(torch).time(fn, 20, warmup=3)
     kv_bytes = int(ctx.sum()) * KV * D * 2 * eb
     name = "fp8" if fp8 else "bf16"
     return {f"decode_{name}_us": round(t * 1e3, 1),
