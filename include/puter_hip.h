@@ -215,6 +215,23 @@ PUTER_API int puter_hip_kv_page_gather(const void *storage, const int32_t *page_
                              int64_t page_count, int64_t page_size, int64_t inner,
                              int64_t out_rows, int64_t storage_offset, int dtype, void *stream);
 
+/* Extension (no reference method): KVPageWrite into an fp8-E4M3 pool with
+ * quantisation.  The reference writes rows in the storage dtype
+ * (execution/page_intrinsic.go:135-215, device/cpu/shape/page_generic.go:5-43);
+ * this hook takes bf16 / f16 / f32 value rows [value_rows, kv_heads * head_dim]
+ * and stores byte = E4M3(value / scale[kv head]) (IEEE f32 division, then the
+ * library's saturating round-to-nearest-even narrowing) at page page_ids[r],
+ * slot offsets[r] of the pool [pages, page_size, kv_heads, head_dim] that starts
+ * storage_offset bytes into `storage`.  It is the inverse of the paged decode's
+ * dequantisation decode(byte) * scale.  Written in place (the device caller's
+ * output == storage, page_intrinsic.go:199-205); rows whose page id or slot is
+ * out of range are skipped. */
+PUTER_API int puter_hip_kv_page_write_fp8(void *storage, const void *values, const int32_t *page_ids,
+                                          const int32_t *offsets, int64_t page_count, int64_t page_size,
+                                          int64_t kv_heads, int64_t head_dim, int64_t value_rows,
+                                          int64_t storage_offset, const float *scales, int value_dtype,
+                                          void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* Attention: device/interface.go:91-110                                      */
 /* ------------------------------------------------------------------------ */

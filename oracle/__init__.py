@@ -64,6 +64,7 @@ def lib():
         _lib.or_unary.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int]
         _lib.or_page_write.argtypes = [C.c_void_p] * 5 + [C.c_int64] * 5 + [C.c_int]
         _lib.or_page_gather.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 6 + [C.c_int]
+        _lib.or_page_write_fp8.argtypes = [C.c_void_p] * 4 + [C.c_int64] * 6 + [C.c_void_p, C.c_int]
         _lib.or_mha.argtypes = [C.POINTER(MHAConfig)] + [C.c_void_p] * 4 + [C.c_int64, C.c_int64, C.c_int]
         _lib.or_mha_rows.argtypes = ([C.POINTER(MHAConfig)] + [C.c_void_p] * 4 +
                                      [C.c_int64] * 6 + [C.c_int])
@@ -232,6 +233,23 @@ def page_write(storage, values, page_ids, offsets, page_size, inner, storage_off
     _check(lib().or_page_write(_p(storage), _p(values), _p(page_ids), _p(offsets), _p(out),
                                page_count, page_size, inner, page_ids.size, storage_offset, es),
            "page_write")
+    return out
+
+
+def page_write_fp8(storage, values, page_ids, offsets, page_size, kv_heads, head_dim, scales,
+                   value_dtype, storage_offset=0, page_count=None):
+    """fp8-E4M3 quantising page write (library extension): returns a new uint8
+    storage with byte = E4M3(x / scale[head]) written at each row's page slot."""
+    storage = _c(storage, np.uint8); values = _c(values)
+    page_ids = _c(page_ids, np.int32); offsets = _c(offsets, np.int32)
+    scales = _c(scales, np.float32)
+    out = storage.copy()
+    inner = kv_heads * head_dim
+    if page_count is None:
+        page_count = (storage.size - storage_offset) // (page_size * inner)
+    _check(lib().or_page_write_fp8(_p(out), _p(values), _p(page_ids), _p(offsets), page_count,
+                                   page_size, kv_heads, head_dim, page_ids.size, storage_offset,
+                                   _p(scales), value_dtype), "page_write_fp8")
     return out
 
 

@@ -121,6 +121,10 @@ int or_page_write(const void *storage, const void *values, const int32_t *page_i
 int or_page_gather(const void *storage, const int32_t *page_table, void *output,
                    int64_t page_count, int64_t page_size, int64_t inner, int64_t out_rows,
                    int64_t storage_offset, int64_t table_len, int elem_size);
+int or_page_write_fp8(uint8_t *storage, const void *values, const int32_t *page_ids,
+                      const int32_t *offsets, int64_t page_count, int64_t page_size,
+                      int64_t kv_heads, int64_t head_dim, int64_t value_rows,
+                      int64_t storage_offset, const float *scales, int value_dtype);
 
 /* ---- attention.c ---- */
 typedef struct {

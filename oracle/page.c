@@ -48,3 +48,29 @@ int or_page_gather(const void *storage, const int32_t *page_table, void *output,
     }
     return 0;
 }
+
+/* fp8 quantising page write (the library's extension hook
+ * puter_hip_kv_page_write_fp8; no reference method): byte = E4M3(x / scale[h])
+ * with IEEE f32 division and the saturating RNE narrowing of or_f32_to_e4m3,
+ * h = element / head_dim.  Row placement and bounds as or_page_write
+ * (page_generic.go:5-43, page.go:139-146).  In place. */
+int or_page_write_fp8(uint8_t *storage, const void *values, const int32_t *page_ids,
+                      const int32_t *offsets, int64_t page_count, int64_t page_size,
+                      int64_t kv_heads, int64_t head_dim, int64_t value_rows,
+                      int64_t storage_offset, const float *scales, int value_dtype) {
+    if (page_count < 0 || page_size <= 0 || kv_heads <= 0 || head_dim <= 0 || value_rows < 0) return -6;
+    for (int64_t r = 0; r < value_rows; ++r) {
+        if (page_ids[r] < 0 || page_ids[r] >= page_count) return -6;
+        if (offsets[r] < 0 || offsets[r] >= page_size) return -6;
+    }
+    const int64_t inner = kv_heads * head_dim;
+    uint8_t *dst = storage + storage_offset;
+    for (int64_t r = 0; r < value_rows; ++r) {
+        uint8_t *row = dst + ((int64_t)page_ids[r] * page_size + offsets[r]) * inner;
+        for (int64_t e = 0; e < inner; ++e) {
+            const float x = or_load(values, (size_t)(r * inner + e), value_dtype);
+            row[e] = or_f32_to_e4m3(x / scales[e / head_dim]);
+        }
+    }
+    return 0;
+}

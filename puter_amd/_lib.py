@@ -76,6 +76,7 @@ SIGNATURES = {
     "puter_hip_cast": ([vp, i32, vp, i32, i64, vp], i32),
     "puter_hip_kv_page_write": ([vp] * 5 + [i64] * 5 + [i32, vp], i32),
     "puter_hip_kv_page_gather": ([vp] * 3 + [i64] * 5 + [i32, vp], i32),
+    "puter_hip_kv_page_write_fp8": ([vp] * 4 + [i64] * 6 + [vp, i32, vp], i32),
     "puter_hip_multi_head_attention": ([C.POINTER(MHAConfig), vp, vp, vp, vp, i64, i64, i32, vp],
                                        i32),
     "puter_hip_multi_head_attention_batched": ([C.POINTER(MHAConfig), vp, vp, vp, vp, i64, i64,

@@ -276,6 +276,15 @@ class Backend:
                                                 pageCount, pageSize, inner, outRows,
                                                 storageOffset, format, self.stream()))
 
+    def KVPageWriteFP8(self, storage, values, pageIDs, offsets, pageCount, pageSize, kvHeads,
+                       headDim, valueRows, storageOffset, scales, valueFormat):
+        """Extension hook (no reference method): quantise bf16 / f16 / f32 rows into
+        an fp8-E4M3 pool, byte = E4M3(value / scales[kv head]), in place."""
+        check(self.lib.puter_hip_kv_page_write_fp8(_ptr(storage), _ptr(values), _ptr(pageIDs),
+                                                   _ptr(offsets), pageCount, pageSize, kvHeads,
+                                                   headDim, valueRows, storageOffset, _ptr(scales),
+                                                   valueFormat, self.stream()))
+
     # ---- Attention: device/interface.go:91-110 ----
     @staticmethod
     def _mha(config):

@@ -49,6 +49,43 @@ __global__ __launch_bounds__(256) void page_write_kernel(char *__restrict__ stor
     for (int64_t u = lane; u < row_units; u += 64) dst[u] = src[u];
 }
 
+// fp8 quantising write: one wave per value row; lane handles 16 consecutive
+// elements at a time (one 16-byte fp8 store; head = element / head_dim).
+template <int DT>
+__global__ __launch_bounds__(256) void page_write_fp8_kernel(uint8_t *__restrict__ storage,
+                                                             const void *__restrict__ values,
+                                                             const int32_t *__restrict__ ids,
+                                                             const int32_t *__restrict__ offsets,
+                                                             const float *__restrict__ scales,
+                                                             int64_t page_count, int64_t page_size,
+                                                             int64_t head_dim, int64_t inner, int64_t value_rows) {
+    using T = typename Elem<DT>::T;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= value_rows) return;
+    const int32_t id = ids[row], off = offsets[row];
+    if (id < 0 || id >= page_count || off < 0 || off >= page_size) return;
+    uint8_t *dst = storage + ((int64_t)id * page_size + off) * inner;
+    const T *src = reinterpret_cast<const T *>(values) + row * inner;
+    for (int64_t e0 = (int64_t)lane * 16; e0 < inner; e0 += 64 * 16) {
+        uint32_t w[4] = {0, 0, 0, 0};
+        const int n = (int)min((int64_t)16, inner - e0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (i < n) {
+                const int64_t e = e0 + i;
+                const float q = __fdiv_rn(Elem<DT>::load(src[e]), scales[e / head_dim]);
+                w[i >> 2] |= f32_to_e4m3(q) << (8 * (i & 3));
+            }
+        }
+        if (n == 16) {
+            *reinterpret_cast<uint4 *>(dst + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            for (int i = 0; i < n; ++i) dst[e0 + i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+        }
+    }
+}
+
 static bool all_aligned(const void *const *p, int n, uintptr_t mask) {
     for (int i = 0; i < n; ++i)
         if (reinterpret_cast<uintptr_t>(p[i]) & mask) return false;
@@ -94,6 +131,31 @@ int puter_hip_kv_page_write(const void *storage, const void *values, const int32
         page_write_kernel<uint8_t><<<blocks, 256, 0, s>>>(dst_base, (const char *)values, page_ids, offsets,
                                                           page_count, page_size, (int64_t)row_bytes, value_rows);
     return check_launch("kv page write");
+}
+
+int puter_hip_kv_page_write_fp8(void *storage, const void *values, const int32_t *page_ids,
+                                const int32_t *offsets, int64_t page_count, int64_t page_size,
+                                int64_t kv_heads, int64_t head_dim, int64_t value_rows,
+                                int64_t storage_offset, const float *scales, int value_dtype,
+                                void *stream) {
+    if (!is_norm_dtype(value_dtype)) return fail(PUTER_ERR_INVALID, "kv page write fp8: unsupported value dtype %d", value_dtype);
+    if (page_count < 0 || page_size <= 0 || kv_heads <= 0 || head_dim <= 0 || value_rows < 0 || storage_offset < 0)
+        return fail(PUTER_ERR_INVALID, "kv page write fp8: invalid shape");
+    if (value_rows == 0) return PUTER_OK;
+    if (!storage || !values || !page_ids || !offsets || !scales) return fail(PUTER_ERR_NIL, "kv page write fp8: nil buffer");
+    const int64_t inner = kv_heads * head_dim;
+    uint8_t *dst = static_cast<uint8_t *>(storage) + storage_offset;
+    // the 16-byte fp8 stores need 16-byte aligned rows
+    if (((reinterpret_cast<uintptr_t>(dst) | (uintptr_t)inner) & 15) != 0)
+        return fail(PUTER_ERR_INVALID, "kv page write fp8: pool rows must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const unsigned blocks = (unsigned)((value_rows + 3) / 4);
+    switch (value_dtype) {
+    case PUTER_F32: page_write_fp8_kernel<PUTER_F32><<<blocks, 256, 0, s>>>(dst, values, page_ids, offsets, scales, page_count, page_size, head_dim, inner, value_rows); break;
+    case PUTER_BF16: page_write_fp8_kernel<PUTER_BF16><<<blocks, 256, 0, s>>>(dst, values, page_ids, offsets, scales, page_count, page_size, head_dim, inner, value_rows); break;
+    case PUTER_F16: page_write_fp8_kernel<PUTER_F16><<<blocks, 256, 0, s>>>(dst, values, page_ids, offsets, scales, page_count, page_size, head_dim, inner, value_rows); break;
+    }
+    return check_launch("kv page write fp8");
 }
 
 int puter_hip_kv_page_gather(const void *storage, const int32_t *page_table, void *output,

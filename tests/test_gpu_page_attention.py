@@ -68,6 +68,57 @@ def test_page_gather_identity_table_is_contiguous_copy(backend):
     assert np.array_equal(to_host(out, np.float32).ravel(), storage)
 
 
+@pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
+def test_page_write_fp8_matches_oracle(backend, dt):
+    """Extension hook: quantising write into an fp8-E4M3 pool [pages, 16, 4, 128],
+    bit-exact against the oracle (IEEE division, saturating RNE narrowing),
+    including values beyond the E4M3 range (saturation) and a layer offset."""
+    rng = np.random.default_rng(31 + dt)
+    pages, ps, kvh, hd = 24, 16, 4, 128
+    inner = kvh * hd
+    layer_off = pages * ps * inner                # second layer of a rank-5 storage
+    storage = rng.integers(0, 256, size=2 * pages * ps * inner).astype(np.uint8)
+    rows = 100
+    slots = rng.choice(pages * ps, size=rows, replace=False)      # unique (page, slot)
+    ids = (slots // ps).astype(np.int32)
+    offs = (slots % ps).astype(np.int32)
+    scales = rng.uniform(0.01, 1.0, kvh).astype(np.float32)
+    x = rng.normal(0, 1, (rows, inner)).astype(np.float32) * 200.0   # |x / s| up to ~1e5: saturates
+    vals = encode(x, dt)
+    ref = O.page_write_fp8(storage, vals, ids, offs, ps, kvh, hd, scales, dt, storage_offset=layer_off)
+    d = to_dev(storage)
+    backend.KVPageWriteFP8(d, to_dev(vals), to_dev(ids), to_dev(offs), pages, ps, kvh, hd, rows,
+                           layer_off, to_dev(scales), dt)
+    got = to_host(d, np.uint8)
+    assert np.array_equal(got, ref)
+
+
+def test_page_write_fp8_roundtrip_and_bounds(backend):
+    """Dequantised pool rows equal the values within E4M3's half-ulp (2^-4 relative
+    for normal codes); rows with a bad page id or slot leave the pool untouched."""
+    rng = np.random.default_rng(7)
+    pages, ps, kvh, hd = 8, 16, 2, 64
+    inner = kvh * hd
+    storage = np.zeros(pages * ps * inner, np.uint8)
+    scales = np.array([0.5, 0.03125], np.float32)
+    x = rng.normal(0, 1, (4, inner)).astype(np.float32)
+    vals = encode(x, O.BF16)
+    ids = np.array([3, 99, 5, -1], np.int32)      # rows 1 and 3 are out of range
+    offs = np.array([2, 0, 15, 4], np.int32)
+    d = to_dev(storage)
+    backend.KVPageWriteFP8(d, to_dev(vals), to_dev(ids), to_dev(offs), pages, ps, kvh, hd, 4, 0,
+                           to_dev(scales), O.BF16)
+    got = to_host(d, np.uint8).reshape(pages, ps, inner)
+    touched = np.zeros((pages, ps), bool)
+    touched[3, 2] = touched[5, 15] = True
+    assert not got[~touched].any(), "an out-of-range row was written"
+    xs = decode(vals, O.BF16)
+    for r, (pg, sl) in ((0, (3, 2)), (2, (5, 15))):
+        deq = O.to_f32(got[pg, sl], O.F8E4M3).reshape(kvh, hd) * scales[:, None]
+        want = xs[r].reshape(kvh, hd)
+        assert np.all(np.abs(deq - want) <= np.abs(want) * 2.0 ** -4 + scales[:, None] * 2.0 ** -9)
+
+
 def test_page_out_of_range_ids_never_touch_memory(backend):
     pages, ps, inner = 4, 2, 8
     storage = seeded(4, (pages * ps * inner,))

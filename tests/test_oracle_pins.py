@@ -449,3 +449,38 @@ def test_paged_decode_matches_gather_then_mha():
 def test_matmul_f64():
     a, b = seeded(1, (9, 17)), seeded(2, (17, 5))
     assert np.max(np.abs(O.matmul_f32(a, b) - a.astype(np.float64) @ b)) < 1e-5
+
+
+# ------------------------------------------------ fp8 quantising page write --
+def _write_fp8_one(values_f32, scales, head_dim):
+    """One row, one page of one slot: returns the written bytes."""
+    kvh = len(scales)
+    storage = np.zeros(kvh * head_dim, np.uint8)
+    return O.page_write_fp8(storage, np.asarray(values_f32, np.float32).reshape(1, -1),
+                            np.array([0], np.int32), np.array([0], np.int32), 1, kvh, head_dim,
+                            np.asarray(scales, np.float32), O.F32)
+
+
+def test_page_write_fp8_grid_points_are_exact():
+    """x = e4m3 value * 2^k with scale 2^k quantises to exactly that code."""
+    codes = np.array([0x00, 0x01, 0x08, 0x38, 0x39, 0x7E, 0x80, 0xB8, 0xFE], np.uint8)
+    vals = O.to_f32(codes, O.F8E4M3)
+    got = _write_fp8_one(vals * 0.25, [0.25], codes.size)
+    assert np.array_equal(got, codes)
+
+
+def test_page_write_fp8_saturates_and_selects_head_scale():
+    """|x / s| beyond 448 stores the largest finite code (0x7E / 0xFE); head h of a
+    row uses scales[h] (element / head_dim)."""
+    got = _write_fp8_one([1e6, -1e6, 448.0 * 3.0, 1.0], [1.0, 3.0], 2)
+    assert list(got) == [0x7E, 0xFE, 0x7E, 0x2B]   # 1/3 -> 0.34375 = 0x2B (RNE: 0.25 + 2.67 steps of 2^-5)
+
+
+def test_page_write_fp8_divides_rather_than_multiplying_by_reciprocal():
+    """0.341796875 / 7 = 0.048828125 exactly: the tie between codes 0x14 (0.046875)
+    and 0x15 (0.05078125), which RNE sends to the even 0x14.  The product with
+    f32(1/7) lands just above the tie and would give 0x15."""
+    x, s = np.float32(0.341796875), np.float32(7.0)
+    assert x / s == np.float32(0.048828125)
+    assert x * (np.float32(1.0) / s) > np.float32(0.048828125)
+    assert list(_write_fp8_one([x], [s], 1)) == [0x14]
