@@ -8,27 +8,32 @@
 // rows are read straight from the page pools (no materialised [ctx, Hkv*D]
 // copies), so HBM traffic is the KV bytes read once.
 //
-// Split-K ("flash decoding"): grid = (kv head, 256-token splits, batch), the kv
-// head fastest so the blocks reading the 8 head slices of the same pages run
-// together; each of a block's 4 waves owns 64 consecutive tokens.  (An MFMA
-// version of the value product, V^T transposed through LDS, measured slower
-// for bf16: its LDS tile halves the blocks per CU of this memory-bound kernel.)
-//   scores: S^T[token, head] = K . Q^T with v_mfma_f32_16x16x32_bf16 (A = 16
-//     tokens x 32 dims loaded straight from the page pool into registers, B =
-//     the G query heads of the kv group, zero-padded to 16 columns); a lane then
-//     holds 16 scores of one head, so the softmax over the wave's 64 tokens is
-//     an in-lane reduction plus two shuffles - no per-token rescaling.
+// Split-K ("flash decoding"): grid = (kv head, 256-token split, sequence), one
+// wave per block, the kv head fastest so the waves reading the 8 head slices of
+// the same pages run together.  The wave walks its split in 32-token
+// sub-chunks with an online softmax, loading the next sub-chunk's K and V rows
+// while it computes the current one.
+//   loads: every load instruction reads whole KV rows (16 lanes x 16 bytes =
+//     one 256-byte bf16 row), which measured 17-25% faster than loading K in
+//     the MFMA operand layout (16 rows x 64 bytes per instruction) or copying
+//     it HBM -> LDS directly.
+//   scores: S^T[token, head] = K . Q^T with v_mfma_f32_16x16x32_bf16; K rows
+//     reach the operand layout through a wave-private LDS tile (swizzled, bank-
+//     conflict free), B = the G query heads of the kv group, zero-padded to 16
+//     columns; a lane then holds 8 scores of one head.
 //   values: O[head, d] += p[head, token] * V[token, d] on the VALU: lane owns 8
-//     dims of every 4th token (16-byte V loads), reads the token's G
-//     probabilities from a per-wave LDS row, and accumulates G x 8 sums.
-// A wave's 4 token-group partials are summed in registers (lane-row swaps),
-// the 4 waves' partials merge through LDS into one (m, l, o[D]) per query
-// head; decode_combine_kernel merges the splits by log-sum-exp.
+//     dims of every 4th token, reads the token's G probabilities from a
+//     wave-private LDS row, and accumulates G x 8 sums.
+// The 4 token-group partials are summed in registers (lane-row swaps) into one
+// (m, l, o[D]) per query head and split; decode_combine_kernel merges the
+// splits by log-sum-exp.
 #include "common.hpp"
+#include <algorithm>
+#include <type_traits>
 
 namespace puter {
 
-constexpr int kSplit = 256;  // tokens per split (4 waves x 64)
+constexpr int kSplit = 256;  // tokens per split (one wave, 8 sub-chunks of 32)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -45,47 +50,58 @@ struct DecodeArgs {
     float scale;
 };
 
-// 8 consecutive KV elements of one row as bf16.  fp8-E4M3 is widened with the
-// hardware v_cvt_pk_f32_fp8 (OCP E4M3FN on gfx950: exact for every code; every
-// E4M3 value is also a bf16 value, so the narrowing to bf16 is exact too).
-template <int KV>
-__device__ __forceinline__ uint4 load8_as_bf16(const void *pool, size_t elem_off) {
-    if constexpr (KV == PUTER_BF16) {
-        return ld_stream(reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(pool) + elem_off));
-    } else {
-        const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(pool) + elem_off);
-        const uint32_t w[2] = {raw.x, raw.y};
-        uint32_t o[4];
+// 8 fp8-E4M3 codes (8 bytes) -> 8 bf16.  The hardware v_cvt_pk_f32_fp8 decodes
+// OCP E4M3FN on gfx950 (exact for every code); every E4M3 value is also a bf16
+// value, so the narrowing to bf16 is exact too.
+__device__ __forceinline__ uint4 fp8x8_to_bf16(uint2 raw) {
+    const uint32_t w[2] = {raw.x, raw.y};
+    uint32_t o[4];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);  // bytes 0, 1
-            const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);   // bytes 2, 3
-            const bf16x2_t h0 = {(__bf16)f0[0], (__bf16)f0[1]};
-            const bf16x2_t h1 = {(__bf16)f1[0], (__bf16)f1[1]};
-            o[2 * k] = __builtin_bit_cast(uint32_t, h0);
-            o[2 * k + 1] = __builtin_bit_cast(uint32_t, h1);
-        }
-        return make_uint4(o[0], o[1], o[2], o[3]);
+    for (int k = 0; k < 2; ++k) {
+        const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);  // bytes 0, 1
+        const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);   // bytes 2, 3
+        const bf16x2_t h0 = {(__bf16)f0[0], (__bf16)f0[1]};
+        const bf16x2_t h1 = {(__bf16)f1[0], (__bf16)f1[1]};
+        o[2 * k] = __builtin_bit_cast(uint32_t, h0);
+        o[2 * k + 1] = __builtin_bit_cast(uint32_t, h1);
     }
+    return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// One wave per (kv head, 256-token split, sequence): the split is walked in
+// eight 32-token sub-chunks with an online softmax.  Once sub-chunk n's rows
+// have landed and its K rows are parked in LDS, sub-chunk n+1's K and V rows
+// are loaded (V into a second register set) while n is computed, so every wave
+// keeps a sub-chunk of loads in flight while it works; small registers and LDS
+// let 8 waves share a CU.  Every load instruction
+// reads whole KV rows: lane group grp takes token 4k + grp, lane l16 its 16-byte
+// (bf16) or 8-byte (fp8) piece l16.  K rows then pass through a wave-private
+// LDS tile (piece p of row r stored at p ^ swizzle(r)) to reach the MFMA
+// operand layout, 16 rows x one piece per read, bank-conflict free.
 template <int KV, int G>
-__global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
-    constexpr int D = 128;
-    __shared__ float p_lds[4][64][G];          // per wave: probabilities [token][head]
-    __shared__ float red_m[4][G], red_l[4][G];
-    __shared__ float red_o[4][G][D];           // [wave][head][d], token groups already summed
+__global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a) {
+    constexpr int D = 128, SUB = 32, NSUB = kSplit / SUB, NGRP = kSplit / 64;
+    constexpr bool BF = KV == PUTER_BF16;
+    constexpr int RB = BF ? 256 : 128;            // KV row bytes
+    using VT = typename std::conditional<BF, uint4, uint2>::type;
+    __shared__ __attribute__((aligned(1024))) char k_lds[SUB * RB];
+    __shared__ float p_lds[SUB][G];               // probabilities [token][head]
 
     const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
     const int ctx = (int)min((int64_t)a.ctx[b], a.max_context);
     const int t0 = split * kSplit;
     if (t0 >= ctx) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int l16 = lane & 15, grp = lane >> 4;
+    const int lane = threadIdx.x, l16 = lane & 15, grp = lane >> 4;
+    const int nsub = min(NSUB, (ctx - t0 + SUB - 1) / SUB);
     const int64_t inner = a.kv_heads * D;
     const int ps = (int)a.page_size;
     const int32_t *table = a.table + (int64_t)b * a.max_pages;
-    const int tw0 = t0 + wave * 64;
+    const int64_t head_off = (int64_t)kvh * D;
+    const uint8_t *kpool = static_cast<const uint8_t *>(a.kp);
+    const uint8_t *vpool = static_cast<const uint8_t *>(a.vp);
+    constexpr int EB = BF ? 2 : 1;
+    // byte offset of this lane's piece of pool row `row`
+    auto piece = [&](int row) -> int64_t { return ((int64_t)row * inner + head_off) * EB + (int64_t)sizeof(VT) * l16; };
 
     // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero
     bf16x8_t qb[4];
@@ -96,105 +112,149 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             u = *reinterpret_cast<const uint4 *>(a.q + ((int64_t)b * a.heads + (int64_t)kvh * G + l16) * D + 32 * t + 8 * grp);
         qb[t] = __builtin_bit_cast(bf16x8_t, u);
     }
-
-    // Token resolution, once per lane: lane L owns token tw0 + L and looks up
-    // its page (one coalesced read of the page-table row); the pool row index
-    // (page * page_size + slot, -1 for dead tokens and bad page ids, which are
-    // masked and never read) is then passed to the lanes that load that token
-    // by a cross-lane shuffle.
-    int myrow = -1;
-    {
-        const int tok = tw0 + lane;
+    // pool rows of the lane's tokens t0 + 64m + lane (-1: past the context or a
+    // bad page id); sub-chunk n holds tokens 32(n%2) .. +31 of group m = n/2
+    int myrow[NGRP];
+#pragma unroll
+    for (int n = 0; n < NGRP; ++n) {
+        myrow[n] = -1;
+        const int tok = t0 + 64 * n + lane;
         if (tok < ctx) {
             const int pidx = tok / ps;
             const int32_t page = table[pidx];
-            if (page >= 0 && page < a.num_pages) myrow = page * ps + (tok - pidx * ps);
+            if (page >= 0 && page < a.num_pages) myrow[n] = page * ps + (tok - pidx * ps);
         }
     }
-    const int64_t head_off = (int64_t)kvh * D;
-    auto row_off = [&](int row) -> int64_t { return (int64_t)row * inner + head_off; };
 
-    // K rows for the wave's 4 tiles of 16 tokens (A operand: token l16, dims 32t + 8grp)
-    f32x4_t s[4];
-    bool klive[4];
+    VT kbuf[8], vbuf[2][8];   // rows of tokens 4k + grp of a sub-chunk, piece l16
+    // issue sub-chunk n's K and V row loads (dead rows, including whole
+    // sub-chunks past the context, read pool row 0, an L2 hit: their scores
+    // are masked and their V rows zeroed; the launcher never runs this kernel
+    // on an empty pool)
+    auto issue = [&](int n, VT (&kb)[8], VT (&vb)[8]) __attribute__((always_inline)) {
+        const int src = myrow[n >> 1], base = 32 * (n & 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = __shfl(myrow, 16 * i + l16, 64);
-        klive[i] = row >= 0;
-        const int64_t off = klive[i] ? row_off(row) : 0;
-        s[i] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint4 kv = load8_as_bf16<KV>(a.kp, (size_t)(off + 32 * t + 8 * grp));
-            s[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], s[i], 0, 0, 0);
+        for (int k = 0; k < 8; ++k) {
+            const int64_t off = piece(max(__shfl(src, base + 4 * k + grp, 64), 0));
+            if constexpr (BF) {
+                kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
+                vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
+            } else {
+                kb[k] = *reinterpret_cast<const uint2 *>(kpool + off);
+                vb[k] = *reinterpret_cast<const uint2 *>(vpool + off);
+            }
         }
-    }
-    // V rows this lane accumulates: tokens tw0 + 4k + grp, dims 8*l16 .. +7
-    uint4 vv[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const int row = __shfl(myrow, 4 * k + grp, 64);
-        const int64_t off = row >= 0 ? row_off(row) : 0;
-        const uint4 v = load8_as_bf16<KV>(a.vp, (size_t)(off + 8 * l16));
-        vv[k] = row >= 0 ? v : make_uint4(0, 0, 0, 0);   // masked rows contribute exact zeros
-    }
+    };
 
-    // softmax over the wave's 64 tokens; lane's scores: head l16, tokens 16i + 4grp + r
-    const float kscale = KV == PUTER_BF16 ? 1.0f : a.ks[kvh];
+    const float kscale = BF ? 1.0f : a.ks[kvh];
     const float c = a.scale * kscale * 1.4426950408889634f;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tok = tw0 + 16 * i + 4 * grp + r;
-            float v = s[i][r];
-            if constexpr (KV == PUTER_BF16) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
-            // liveness of this token: the tile's K row owner is lane (4grp + r) of the 16
-            const bool live = __shfl(klive[i] ? 1 : 0, 4 * grp + r, 16) != 0;
-            v = live ? v * c : -INFINITY;
-            s[i][r] = v;
-            mx = fmaxf(mx, v);
-        }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mref = mx == -INFINITY ? 0.0f : mx;
-    float lsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float p = s[i][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i][r] - mref);
-            lsum += p;
-            if (l16 < G) p_lds[wave][16 * i + 4 * grp + r][l16] = p;
-        }
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-
-    // O partial for token group grp: acc[h][j] = sum_k p[h][4k+grp] * V[4k+grp][8 l16 + j]
+    float m_run = -INFINITY, l_run = 0.0f;   // head l16's running max (log2 domain) and sum
     float acc[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
+
+    // sub-chunk n: wait for its rows, move its K rows into the LDS tile (which
+    // frees the K registers), issue sub-chunk n+1, then compute n
+    issue(0, kbuf, vbuf[0]);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        float v[8];
-        unpack_vec<PUTER_BF16>(vv[k], v);
-        float p[G];
+    for (int n = 0; n < NSUB; ++n) {
+        if (n >= nsub) break;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): sub-chunk n's loads have landed
+        VT (&vc)[8] = vbuf[n & 1];
+        // K rows -> LDS tile (row r = 4k + grp, piece l16 at l16 ^ swizzle(r))
 #pragma unroll
-        for (int h = 0; h < G; ++h) p[h] = p_lds[wave][4 * k + grp][h];
+        for (int k = 0; k < 8; ++k) {
+            const int r = 4 * k + grp;
+            if constexpr (BF) *reinterpret_cast<uint4 *>(k_lds + r * 256 + ((l16 ^ (r & 15)) << 4)) = kbuf[k];
+            else *reinterpret_cast<uint2 *>(k_lds + r * 128 + ((l16 ^ ((r >> 1) & 7)) << 3)) = kbuf[k];
+        }
+        if (n + 1 < NSUB) issue(n + 1, kbuf, vbuf[(n + 1) & 1]);
+        __builtin_amdgcn_wave_barrier();   // the tile is private to this wave; LDS ops run in order
+        // token t of the sub-chunk is live iff bit t
+        const uint64_t live = __ballot(myrow[n >> 1] >= 0) >> (32 * (n & 1));
+        const uint64_t liveg = live >> (4 * grp);   // score (i, r): token 16i + 4grp + r
+        const uint64_t livev = live >> grp;         // V row k: token 4k + grp
+        // scores: A operand = K tile row 16i + l16, dims 32t + 8grp
+        f32x4_t s[2];
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+        for (int i = 0; i < 2; ++i) {
+            s[i] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+            const int row = 16 * i + l16;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(p[h], v[j], acc[h][j]);
+            for (int t = 0; t < 4; ++t) {
+                uint4 kv;
+                if constexpr (BF) {
+                    kv = *reinterpret_cast<const uint4 *>(k_lds + row * 256 + (((4 * t + grp) ^ l16) << 4));
+                } else {
+                    kv = fp8x8_to_bf16(*reinterpret_cast<const uint2 *>(
+                        k_lds + row * 128 + (((4 * t + grp) ^ ((l16 >> 1) & 7)) << 3)));
+                }
+                s[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], s[i], 0, 0, 0);
+            }
+        }
+        // lane's scores: head l16, tokens 16i + 4grp + r
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = s[i][r];
+                if constexpr (BF) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
+                v = ((liveg >> (16 * i + r)) & 1) ? v * c : -INFINITY;
+                s[i][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float mref = m_new == -INFINITY ? 0.0f : m_new;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = s[i][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i][r] - mref);
+                lsum += p;
+                if (l16 < G) p_lds[16 * i + 4 * grp + r][l16] = p;
+            }
+        lsum += __shfl_xor(lsum, 16, 64);
+        lsum += __shfl_xor(lsum, 32, 64);
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+        __builtin_amdgcn_wave_barrier();
+        // rescale by head h's alpha (held by lane h), then accumulate p * V
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float ah = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(alpha), h));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[h][j] *= ah;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t keep = ((livev >> (4 * k)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
+            uint4 w;
+            if constexpr (BF) w = vc[k];
+            else w = fp8x8_to_bf16(vc[k]);
+            w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
+            float v[8];
+            unpack_vec<PUTER_BF16>(w, v);
+            float p[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) p[h] = p_lds[4 * k + grp][h];
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(p[h], v[j], acc[h][j]);
+        }
     }
-    // sum the 4 token groups (16-lane rows) in registers: permlane16_swap pairs
-    // rows (0,1) and (2,3), permlane32_swap then pairs the two halves, leaving
-    // the full sum in every row; row grp stores head grp % G's values
+    // loads issued for a sub-chunk past the context are drained before exit
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    // sum the 4 token groups (16-lane rows): permlane16_swap pairs rows (0,1)
+    // and (2,3), permlane32_swap then pairs the halves; row grp writes head h's
+    // partial for the heads with h % 4 == grp
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -205,34 +265,18 @@ __global__ __launch_bounds__(256) void decode_mfma_kernel(DecodeArgs a) {
             const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
             acc[h][j] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
         }
-    if (lane < G) {  // lanes 0..G-1 hold head l16 = lane with grp 0
-        red_m[wave][lane] = mx;
-        red_l[wave][lane] = lsum;
-    }
+    const int64_t slot0 = ((int64_t)b * a.heads + (int64_t)kvh * G) * a.max_splits + split;
 #pragma unroll
     for (int h = 0; h < G; ++h)
-        if ((h & 3) == grp)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) red_o[wave][h][8 * l16 + j] = acc[h][j];
-    __syncthreads();
-
-    // merge the 4 waves -> one partial per query head
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        const int h = idx / D, d = idx % D;
-        float M = -INFINITY;
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][h]);
-        float L = 0.0f, O = 0.0f;
-        for (int w = 0; w < 4; ++w) {
-            const float f = red_m[w][h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][h] - M);
-            L += red_l[w][h] * f;
-            O += red_o[w][h][d] * f;
+        if ((h & 3) == grp) {
+            float4 *dst = reinterpret_cast<float4 *>(a.part_o + (slot0 + (int64_t)h * a.max_splits) * D + 8 * l16);
+            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
         }
-        const int64_t slot = ((int64_t)b * a.heads + (int64_t)kvh * G + h) * a.max_splits + split;
-        a.part_o[slot * D + d] = O;
-        if (d == 0) {
-            a.part_ml[slot * 2] = M;   // log2-domain max of the scaled scores
-            a.part_ml[slot * 2 + 1] = L;
-        }
+    if (grp == 0 && l16 < G) {
+        const int64_t slot = slot0 + (int64_t)l16 * a.max_splits;
+        a.part_ml[slot * 2] = m_run;   // log2-domain max of the scaled scores
+        a.part_ml[slot * 2 + 1] = l_run;
     }
 }
 
@@ -277,6 +321,12 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
     float r = L > 0.0f ? O / L : 0.0f;
     if constexpr (KV != PUTER_BF16) r *= a.vs[h / (a.heads / a.kv_heads)];
     a.out[((int64_t)b * a.heads + h) * D + d] = (uint16_t)f32_to_bf16(r);
+}
+
+// An empty pool masks every token: the output is zero.
+__global__ __launch_bounds__(256) void decode_zero_kernel(uint16_t *out, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = 0;
 }
 
 static int64_t splits_for(int64_t max_context) { return (max_context + kSplit - 1) / kSplit; }
@@ -330,13 +380,18 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
                  batch, max_pages_per_seq, page_size, num_pages, num_heads, kv_heads, splits,
                  max_context, (float)(1.0 / sqrt((double)head_dim))};
     hipStream_t s = as_stream(stream);
+    if (num_pages == 0) {  // every page id is out of range: all tokens masked
+        const int64_t n = batch * num_heads * head_dim;
+        decode_zero_kernel<<<(unsigned)std::min<int64_t>((n + 255) / 256, 4096), 256, 0, s>>>(static_cast<uint16_t *>(output), n);
+        return check_launch("paged decode");
+    }
     const dim3 grid((unsigned)kv_heads, (unsigned)splits, (unsigned)batch);
 #define PUTER_DECODE(KV)                                                              \
     switch (G) {                                                                      \
-    case 1: decode_mfma_kernel<KV, 1><<<grid, 256, 0, s>>>(a); break;                 \
-    case 2: decode_mfma_kernel<KV, 2><<<grid, 256, 0, s>>>(a); break;                 \
-    case 4: decode_mfma_kernel<KV, 4><<<grid, 256, 0, s>>>(a); break;                 \
-    case 8: decode_mfma_kernel<KV, 8><<<grid, 256, 0, s>>>(a); break;                 \
+    case 1: decode_kernel<KV, 1><<<grid, 64, 0, s>>>(a); break;                       \
+    case 2: decode_kernel<KV, 2><<<grid, 64, 0, s>>>(a); break;                       \
+    case 4: decode_kernel<KV, 4><<<grid, 64, 0, s>>>(a); break;                       \
+    case 8: decode_kernel<KV, 8><<<grid, 64, 0, s>>>(a); break;                       \
     }                                                                                 \
     decode_combine_kernel<KV><<<dim3((unsigned)num_heads, (unsigned)batch), 128, 0, s>>>(a);
     if (kv_dtype == PUTER_BF16) { PUTER_DECODE(PUTER_BF16) }

@@ -258,12 +258,8 @@ def paged_case(seed, batch, ctx_lo, ctx_hi, ps, h, kvh, d, kv_dt):
     return ctx, table, total, q, kp, vp, ks, vs
 
 
-@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
-@pytest.mark.parametrize("batch,lo,hi,ps", [(3, 1, 40, 16), (4, 500, 1300, 16), (2, 256, 256, 16)])
-def test_paged_decode(backend, kv_dt, batch, lo, hi, ps):
-    h, kvh, d = 32, 8, 128
-    ctx, table, total, q, kp, vp, ks, vs = paged_case(batch * 100 + lo, batch, lo, hi, ps, h, kvh, d, kv_dt)
-    ref = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, kv_dt, ks, vs)
+def run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs):
+    batch = len(ctx)
     max_ctx = int(ctx.max())
     ws_bytes = backend.PagedDecodeWorkspaceBytes(batch, h, d, max_ctx)
     ws = empty_dev((ws_bytes // 4,), np.float32)
@@ -272,8 +268,64 @@ def test_paged_decode(backend, kv_dt, batch, lo, hi, ps):
                                  table.shape[1], ps, total, h, kvh, d, max_ctx,
                                  None if ks is None else to_dev(ks), None if vs is None else to_dev(vs),
                                  kv_dt, out, ws, ws_bytes)
-    assert_close(O.to_f32(to_host(out, np.uint16), O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
+    return to_host(out, np.uint16)
+
+
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("batch,lo,hi,ps", [(3, 1, 40, 16), (4, 500, 1300, 16), (2, 256, 256, 16)])
+def test_paged_decode(backend, kv_dt, batch, lo, hi, ps):
+    h, kvh, d = 32, 8, 128
+    ctx, table, total, q, kp, vp, ks, vs = paged_case(batch * 100 + lo, batch, lo, hi, ps, h, kvh, d, kv_dt)
+    ref = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, kv_dt, ks, vs)
+    out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
+    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
                  elem_tol=None, what="paged decode")
+
+
+# group sizes 1, 2, 8 and page sizes that do not divide the 32-token sub-chunks
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("h,kvh", [(8, 8), (8, 4), (16, 2)])
+@pytest.mark.parametrize("ps,lo,hi", [(1, 1, 70), (5, 30, 300), (32, 200, 700)])
+def test_paged_decode_groups_pages(backend, kv_dt, h, kvh, ps, lo, hi):
+    d, batch = 128, 3
+    ctx, table, total, q, kp, vp, ks, vs = paged_case(7000 + 31 * h + kvh + ps, batch, lo, hi, ps, h, kvh, d, kv_dt)
+    ref = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, kv_dt, ks, vs)
+    out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
+    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
+                 elem_tol=None, what="paged decode G=%d ps=%d" % (h // kvh, ps))
+
+
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+def test_paged_decode_bad_page_ids_are_masked(backend, kv_dt):
+    """A token whose page id is outside [0, num_pages) is masked: the result
+    equals attention over the same sequence with that page removed."""
+    h, kvh, d, ps, batch = 16, 4, 128, 16, 2
+    ctx, table, total, q, kp, vp, ks, vs = paged_case(8101, batch, 300, 600, ps, h, kvh, d, kv_dt)
+    bad = table.copy()
+    ref_table = np.zeros_like(table)
+    ref_ctx = ctx.copy()
+    for i in range(batch):
+        npg = (int(ctx[i]) + ps - 1) // ps
+        j = 3 + i                               # a full page inside the context
+        bad[i, j] = -1 if i == 0 else total + 5
+        keep = [table[i, c] for c in range(npg) if c != j]
+        ref_table[i, :len(keep)] = keep
+        ref_ctx[i] = ctx[i] - ps
+    ref = O.paged_decode(q, kp, vp, ref_table, ref_ctx, ps, h, kvh, d, kv_dt, ks, vs)
+    out = run_paged_decode(backend, q, kp, vp, bad, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
+    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
+                 elem_tol=None, what="paged decode, bad page ids")
+
+
+def test_paged_decode_empty_pool(backend):
+    """num_pages = 0: every page id is out of range, every token masked, output 0."""
+    h, kvh, d, ps, batch = 8, 2, 128, 16, 2
+    ctx = np.array([17, 40], np.int32)
+    table = np.zeros((batch, 3), np.int32)
+    q = O.from_f32(seeded(8201, (batch, h * d)), O.BF16)
+    pool = np.zeros((1, ps, kvh, d), np.uint16)   # a valid buffer the kernel must not depend on
+    out = run_paged_decode(backend, q, pool, pool, table, ctx, ps, 0, h, kvh, d, O.BF16, None, None)
+    assert not out.any()
 
 
 def test_matmul_f32(backend):
