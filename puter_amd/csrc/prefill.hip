@@ -40,7 +40,10 @@
 // some query of the wave sees a score more than 2^8 above its reference
 // (wave-uniform branch, rare after the first tiles); otherwise p may exceed 1
 // by at most 2^8, which f32 accumulation and bf16 P absorb exactly as well.
-// The final O / l is the same softmax.
+// The tile max is not even computed on the common path: p is evaluated against
+// the current reference and, as every p is at most its lane's partial row sum,
+// a sum <= 2^8 proves no score crossed the threshold; only otherwise is the max
+// taken and p redone.  The final O / l is the same softmax.
 //
 // Causal blocks visit only the key tiles at or below their diagonal.  Tiles
 // that no query of the block needs masked run a mask-free loop; the few tiles
@@ -63,6 +66,7 @@ constexpr int BM = 128;       // queries per block (4 waves x 32)
 constexpr int BN = 64;        // keys per tile
 constexpr int TILE_BYTES = BN * D * 2;  // one K or V tile in LDS: 16 KB
 constexpr float RESCALE_SLACK = 8.0f;   // log2 headroom before O and l are rescaled
+constexpr float RESCALE_LIMIT = 256.0f; // 2^RESCALE_SLACK: the largest p allowed
 // buffer descriptor word 3 for raw (untyped, stride 0) dword access on gfx9
 constexpr int BUF_WORD3 = 0x00020000;
 }  // namespace fa
@@ -151,35 +155,56 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
             for (int r = 0; r < 16; ++r)
                 s[c][r] = (32 * c + 8 * (r >> 2) + (r & 3)) > lim ? -INFINITY : s[c][r];
     }
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[c][r]);
-    tmax = swap_halves_max(tmax) * a.scale_log2;
-    if (__any(tmax > st.m + RESCALE_SLACK)) {
-        const float mnew = fmaxf(st.m, tmax);
-        const float alpha = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m - mnew);
-        st.m = mnew;
-        st.l *= alpha;
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) st.o[d][r] *= alpha;
-    }
-    const float mref = st.m == -INFINITY ? 0.0f : st.m;
+    // Fast path: every lane already has a reference and p = exp2(s*c - m) is
+    // evaluated without the tile max; since every p <= the row sum, a sum <= 2^8
+    // bounds every p as the max test would.  Otherwise (first tile, or a score
+    // far above the reference) the max is taken, O and l rescaled, p redone.
     float psum = 0.0f;
     bf16x8 pf[2][2];
+    bool done = false;
+    if (!__any(st.m == -INFINITY)) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][8 * h + j], a.scale_log2, -mref));
-                psum += p;
-                pf[c][h][j] = (__bf16)p;  // v_cvt_pk_bf16_f32: round to nearest even
-            }
+                for (int j = 0; j < 8; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][8 * h + j], a.scale_log2, -st.m));
+                    psum += p;
+                    pf[c][h][j] = (__bf16)p;
+                }
+        done = !__any(psum > RESCALE_LIMIT);  // each p of this lane <= its partial sum
+    }
+    if (!done) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[c][r]);
+        tmax = swap_halves_max(tmax) * a.scale_log2;
+        if (__any(tmax > st.m + RESCALE_SLACK)) {
+            const float mnew = fmaxf(st.m, tmax);
+            const float alpha = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m - mnew);
+            st.m = mnew;
+            st.l *= alpha;
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st.o[d][r] *= alpha;
+        }
+        const float mref = st.m == -INFINITY ? 0.0f : st.m;
+        psum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][8 * h + j], a.scale_log2, -mref));
+                    psum += p;
+                    pf[c][h][j] = (__bf16)p;
+                }
+    }
     st.l += psum;
     // O^T[d, q] += V^T[d, keys] . P^T[keys, q]: the V^T fragment (dims 32d +
     // lane%32, keys 32c + 16h + 4g + 0..3 and + 8) is two transposing reads
