@@ -142,7 +142,29 @@ def rope_swiglu_casts(torch, be, puter):
         t2 = timer.time(lambda: be.Cast(f32, puter.F32, buf, fmt, gate.numel()), 10)
         res[f"cast_f32_to_{name}_GBs"] = round((4 + eb) * gate.numel() / (t1 * 1e-3) / 1e9, 1)
         res[f"cast_{name}_to_f32_GBs"] = round((4 + eb) * gate.numel() / (t2 * 1e-3) / 1e9, 1)
-    del q, k, gate, up, act, f32, narrow, n8
+    # integer quantisation over the same 117 M elements: Quant (f32 -> int8, 5 B/elem),
+    # Dequant (int8 -> f32, 5 B/elem), Dequant4 (packed int4 -> f32, 4.5 B/elem),
+    # and the f32 <-> f64 casts (12 B/elem)
+    n = gate.numel()
+    i8 = n8.view(torch.int8)
+    q8 = puter.DequantInt8Config(0.05, 3)
+    # Quant's input: fresh N(0,1) f32 (the buffer above holds fp8-rounded values,
+    # half of which divide to exact .5 ties that take the exact-division path)
+    f32.normal_(generator=gen)
+    t = timer.time(lambda: be.Quant(i8, f32, n, q8, puter.I8, puter.F32), 10, warmup=2)
+    res["quant_f32_to_int8_GBs"] = round(5 * n / (t * 1e-3) / 1e9, 1)
+    t = timer.time(lambda: be.Dequant(f32, i8, n, q8, puter.F32, puter.I8), 10, warmup=2)
+    res["dequant_int8_to_f32_GBs"] = round(5 * n / (t * 1e-3) / 1e9, 1)
+    t = timer.time(lambda: be.Dequant4(f32, n8, n, puter.DequantInt4Config(0.25, 0), puter.F32, puter.I4), 10, warmup=2)
+    res["dequant4_int4_to_f32_GBs"] = round(4.5 * n / (t * 1e-3) / 1e9, 1)
+    del narrow, n8, i8
+    torch.cuda.empty_cache()
+    f64 = torch.empty(n, device="cuda", dtype=torch.float64)
+    t = timer.time(lambda: be.Cast(f64, puter.F64, f32, puter.F32, n), 10, warmup=2)
+    res["cast_f32_to_f64_GBs"] = round(12 * n / (t * 1e-3) / 1e9, 1)
+    t = timer.time(lambda: be.Cast(f32, puter.F32, f64, puter.F64, n), 10, warmup=2)
+    res["cast_f64_to_f32_GBs"] = round(12 * n / (t * 1e-3) / 1e9, 1)
+    del q, k, gate, up, act, f32, f64
     torch.cuda.empty_cache()
     return res
 

@@ -45,6 +45,9 @@ enum puter_dtype {
     PUTER_F8E4M3 = 3, /* OCP E4M3FN: bias 7, no Inf, NaN = S.1111.111 */
     PUTER_F8E5M2 = 4, /* OCP E5M2: bias 15, IEEE-like Inf/NaN */
     PUTER_I32 = 5,
+    PUTER_I8 = 6,
+    PUTER_I4 = 7,     /* packed signed nibbles: element 2k = low nibble of byte k, 2k+1 = high */
+    PUTER_F64 = 8,
 };
 
 enum puter_status {
@@ -191,9 +194,13 @@ PUTER_API int puter_hip_unary(int kind, void *dst, const void *src, int64_t coun
 /* ------------------------------------------------------------------------ */
 /* Casts: convert/ package (BFloat16ToFloat32 bf16_f32.go:11, Float32ToBFloat16   */
 /* :21, Float16ToFloat32/Float32ToFloat16 f16_f32.go:10-42,                   */
-/* Float8E4M3ToFloat32/Float32ToFloat8E4M3/E5M2 fp8_f32.go:8-65).             */
-/* One of src_dtype / dst_dtype must be F32.  Bit-exact element-wise rules:  */
-/* RNE narrowing; fp8 saturating; NaN kept as NaN.                           */
+/* Float8E4M3ToFloat32/Float32ToFloat8E4M3/E5M2 fp8_f32.go:8-65,              */
+/* Int8ToFloat32 / Float32ToInt8 / Int4ToFloat32 int_f32.go:14-77,             */
+/* Float32ToFloat64 / Float64ToFloat32 f32_f64.go:8-17).                       */
+/* One of src_dtype / dst_dtype must be F32 (I4 only as a source; count is    */
+/* the element count, the I4 source holds (count+1)/2 bytes).  Bit-exact      */
+/* element-wise rules: RNE narrowing; fp8 saturating; NaN kept as NaN; int8   */
+/* saturating then truncating toward zero, NaN -> 0.                          */
 /* ------------------------------------------------------------------------ */
 PUTER_API int puter_hip_cast(void *dst, int dst_dtype, const void *src, int src_dtype, int64_t count,
                    void *stream);
@@ -301,6 +308,25 @@ PUTER_API int puter_hip_paged_decode_attention(const void *query, const void *ke
                                      int64_t max_context, const float *k_scale,
                                      const float *v_scale, int kv_dtype, void *output,
                                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Integer quantisation: Dequant / Dequant4 device/interface.go:196-199,       */
+/* Quant :580-582 (config = DequantInt8Config{Scale, ZeroPoint} by value,     */
+/* device/config.go:268-276; zero_point must fit int8).                       */
+/* ------------------------------------------------------------------------ */
+/* Dequant: F32 <- I8 only (device/cpu/dequant/ops.go:11-37):
+ * dst[i] = float32(src[i] - zero_point) * scale. */
+PUTER_API int puter_hip_dequant(void *dst, const void *src, int64_t count, float scale,
+                                int32_t zero_point, int dst_dtype, int src_dtype, void *stream);
+/* Dequant4: F32 <- I4 only (dequant/ops.go:39-58): pair_count elements read
+ * from (pair_count+1)/2 packed bytes, dst[i] = float32(nibble(i) - zero_point) * scale. */
+PUTER_API int puter_hip_dequant4(void *dst, const void *src, int64_t pair_count, float scale,
+                                 int32_t zero_point, int dst_dtype, int src_dtype, void *stream);
+/* Quant: I8 <- F32 only (device/cpu/quant/ops.go:10-37, int8_generic.go:5-18):
+ * round-half-away-from-zero(src / scale) + zero_point, saturated to [-128, 127]
+ * (f32 division; NaN -> 0). */
+PUTER_API int puter_hip_quant(void *dst, const void *src, int64_t count, float scale,
+                              int32_t zero_point, int dst_dtype, int src_dtype, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Matmul: device/interface.go:409-415 (F32), device/cpu/matmul/compute.go:46-62 */

@@ -15,7 +15,7 @@ import numpy as np
 
 from .build import LIBRARY, build
 
-F32, F16, BF16, F8E4M3, F8E5M2, I32 = 0, 1, 2, 3, 4, 5
+F32, F16, BF16, F8E4M3, F8E5M2, I32, I8, I4, F64 = 0, 1, 2, 3, 4, 5, 6, 7, 8
 GATE_SWIGLU, GATE_GEGLU, GATE_GEGLU_TANH, GATE_SIGLU, GATE_GLU, GATE_REGLU, GATE_LINGLU = range(7)
 UNARY_SILU, UNARY_GELU = 0, 1
 
@@ -75,6 +75,9 @@ def lib():
         _lib.or_matmul_f32.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 3
         _lib.or_cast_to_f32.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
         _lib.or_cast_from_f32.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        for name in ("or_dequant_int8", "or_dequant_int4", "or_quant_int8"):
+            getattr(_lib, name).argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_float, C.c_int]
+        _lib.or_cast_ext.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_size_t]
         _lib.oracle_set_threads.argtypes = [C.c_int]
         _lib.oracle_get_threads.restype = C.c_int
     return _lib
@@ -311,6 +314,43 @@ def paged_decode(q, key_pages, value_pages, page_table, context_lens, page_size,
                                  _p(context_lens), batch, max_pages, page_size, num_heads, kv_heads,
                                  head_dim, _p(k_scale), _p(v_scale), kv_dtype, _p(out)),
            "paged_decode")
+    return out
+
+
+def dequant_int8(codes, scale, zero_point):
+    """Dequant (F32 <- Int8): device/cpu/dequant/int8_generic.go:3-7."""
+    codes = _c(codes, np.int8)
+    out = np.empty(codes.shape, np.float32)
+    _check(lib().or_dequant_int8(_p(out), _p(codes), codes.size, scale, zero_point), "dequant_int8")
+    return out
+
+
+def dequant_int4(packed, count, scale, zero_point):
+    """Dequant4 (F32 <- Int4): `count` signed nibbles, element 2k = low nibble of byte k."""
+    packed = _c(packed, np.uint8)
+    assert packed.size >= (count + 1) // 2
+    out = np.empty(count, np.float32)
+    _check(lib().or_dequant_int4(_p(out), _p(packed), count, scale, zero_point), "dequant_int4")
+    return out
+
+
+def quant_int8(values, scale, zero_point):
+    """Quant (Int8 <- F32): device/cpu/quant/int8_generic.go:5-18."""
+    values = _c(values, np.float32)
+    out = np.empty(values.shape, np.int8)
+    _check(lib().or_quant_int8(_p(out), _p(values), values.size, scale, zero_point), "quant_int8")
+    return out
+
+
+_EXT_NP = {F32: np.float32, I8: np.int8, I4: np.uint8, F64: np.float64}
+
+
+def cast_ext(src, src_dtype, dst_dtype, count=None):
+    """convert/int_f32.go and convert/f32_f64.go casts (one side is F32)."""
+    src = _c(src, _EXT_NP[src_dtype])
+    n = src.size if count is None else count
+    out = np.empty(n, _EXT_NP[dst_dtype])
+    _check(lib().or_cast_ext(_p(out), dst_dtype, _p(src), src_dtype, n), "cast_ext")
     return out
 
 

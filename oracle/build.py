@@ -9,7 +9,7 @@ import os
 import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-SOURCES = ["numeric.c", "norm.c", "rope.c", "activation.c", "page.c", "attention.c", "matmul.c"]
+SOURCES = ["numeric.c", "norm.c", "rope.c", "activation.c", "page.c", "attention.c", "matmul.c", "quant.c"]
 LIBRARY = os.path.join(HERE, "liboracle.so")
 
 CFLAGS = [

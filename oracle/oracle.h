@@ -1,7 +1,7 @@
 /*
  * CPU oracle: a plain-C restatement of the reference's device/cpu arithmetic for
  * the hot path (norms, gated residual, RoPE, gated activations, dtype casts,
- * paged KV, multi-head attention, f32 matmul).
+ * paged KV, multi-head attention, f32 matmul, integer quantisation).
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library (puter_amd/) links,
  * loads or calls this code. Only tests/, __graft_entry__.smoke() and bench.py's
@@ -40,6 +40,9 @@ enum {
     OR_F8E4M3 = 3,
     OR_F8E5M2 = 4,
     OR_I32 = 5,
+    OR_I8 = 6,
+    OR_I4 = 7,   /* packed signed nibbles: element 2k = low nibble of byte k */
+    OR_F64 = 8,
 };
 
 void oracle_set_threads(int threads);
@@ -61,6 +64,16 @@ void or_store(void *base, size_t index, float value, int dtype);
 /* bulk casts: src dtype -> f32, f32 -> dst dtype */
 int or_cast_to_f32(float *dst, const void *src, size_t count, int src_dtype);
 int or_cast_from_f32(void *dst, const float *src, size_t count, int dst_dtype);
+
+/* ---- quant.c: integer (de)quantisation, int8 / int4 / f64 casts ---- */
+float or_dequant_int8_one(int8_t code, float scale, int8_t zero_point);
+int or_int4_nibble(const uint8_t *src, size_t index);
+int8_t or_quant_int8_one(float value, float scale, int8_t zero_point);
+int8_t or_f32_to_int8(float value);
+int or_dequant_int8(float *dst, const int8_t *src, size_t count, float scale, int zero_point);
+int or_dequant_int4(float *dst, const uint8_t *src, size_t count, float scale, int zero_point);
+int or_quant_int8(int8_t *dst, const float *src, size_t count, float scale, int zero_point);
+int or_cast_ext(void *dst, int dst_dtype, const void *src, int src_dtype, size_t count);
 
 /* ---- norm.c ---- */
 int or_rmsnorm(const void *input, const void *scale, void *output,

@@ -88,6 +88,9 @@ SIGNATURES = {
     "puter_hip_paged_decode_workspace_bytes": ([i64, i64, i64, i64], sz),
     "puter_hip_paged_decode_attention": ([vp] * 5 + [i64] * 8 + [vp, vp, i32, vp, vp, sz, vp],
                                          i32),
+    "puter_hip_dequant": ([vp, vp, i64, C.c_float, i32, i32, i32, vp], i32),
+    "puter_hip_dequant4": ([vp, vp, i64, C.c_float, i32, i32, i32, vp], i32),
+    "puter_hip_quant": ([vp, vp, i64, C.c_float, i32, i32, i32, vp], i32),
     "puter_hip_matmul": ([vp, vp, vp, i64, i64, i64, i32, vp], i32),
 }
 

@@ -14,7 +14,7 @@ import ctypes as C
 from . import _lib
 from ._lib import check, PuterError  # noqa: F401
 
-F32, F16, BF16, F8E4M3, F8E5M2, I32 = 0, 1, 2, 3, 4, 5
+F32, F16, BF16, F8E4M3, F8E5M2, I32, I8, I4, F64 = 0, 1, 2, 3, 4, 5, 6, 7, 8
 GATE_SWIGLU, GATE_GEGLU, GATE_GEGLU_TANH, GATE_SIGLU, GATE_GLU, GATE_REGLU, GATE_LINGLU = range(7)
 UNARY_SILU, UNARY_GELU = 0, 1
 
@@ -24,7 +24,8 @@ ErrLenMismatch = "convert: length mismatch"  # convert/errors.go:10-15
 def dtype_of(t) -> int:
     import torch
     table = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
-             torch.float8_e4m3fn: F8E4M3, torch.float8_e5m2: F8E5M2, torch.int32: I32}
+             torch.float8_e4m3fn: F8E4M3, torch.float8_e5m2: F8E5M2, torch.int32: I32,
+             torch.int8: I8, torch.float64: F64}
     return table[t.dtype]
 
 
@@ -76,6 +77,18 @@ class MultiHeadAttentionConfig:  # config.go:283-290
     WindowSize: int = 0
     ALiBiSlope: float = 0.0
     KVHeadCount: int = 0
+
+
+@dataclass
+class DequantInt8Config:  # config.go:268-271
+    Scale: float = 1.0
+    ZeroPoint: int = 0
+
+
+@dataclass
+class DequantInt4Config:  # config.go:273-276
+    Scale: float = 1.0
+    ZeroPoint: int = 0
 
 
 @dataclass
@@ -262,6 +275,25 @@ class Backend:
     def Float32ToFloat8E5M2(self, dst, src):
         self._convert(dst, F8E5M2, src, F32)
 
+    def Int8ToFloat32(self, dst, src):  # convert/int_f32.go:14-25
+        self._convert(dst, F32, src, I8)
+
+    def Float32ToInt8(self, dst, src):  # convert/int_f32.go:30-52
+        self._convert(dst, I8, src, F32)
+
+    def Int4ToFloat32(self, dst, src):
+        """convert/int_f32.go:59-77: dst.numel() nibbles from the packed bytes of src
+        (len(dst) may be at most 2 * len(src))."""
+        if dst.numel() > 2 * src.numel():
+            raise ValueError(ErrLenMismatch)
+        self.Cast(dst, F32, src, I4, dst.numel())
+
+    def Float32ToFloat64(self, dst, src):  # convert/f32_f64.go:8-10
+        self._convert(dst, F64, src, F32)
+
+    def Float64ToFloat32(self, dst, src):  # convert/f32_f64.go:15-17
+        self._convert(dst, F32, src, F64)
+
     # ---- paged KV hooks: execution/page_intrinsic.go:13-24 ----
     def KVPageWrite(self, storage, values, pageIDs, offsets, output, pageCount, pageSize, inner,
                     valueRows, storageOffset, format):
@@ -333,6 +365,22 @@ class Backend:
             batch, maxPagesPerSeq, pageSize, numPages, numHeads, kvHeads, headDim, maxContext,
             _ptr(kScale), _ptr(vScale), kvFormat, _ptr(output), _ptr(workspace), workspaceBytes,
             self.stream()))
+
+    # ---- Dequant / Quant: device/interface.go:196-199, 580-582 ----
+    def Dequant(self, dst, src, count, config, dstFormat, srcFormat):
+        """dequant/ops.go:11-37: F32 <- Int8, (src - ZeroPoint) * Scale."""
+        check(self.lib.puter_hip_dequant(_ptr(dst), _ptr(src), count, config.Scale, config.ZeroPoint,
+                                         dstFormat, srcFormat, self.stream()))
+
+    def Dequant4(self, dst, src, pairCount, config, dstFormat, srcFormat):
+        """dequant/ops.go:39-58: F32 <- Int4 (pairCount nibbles, low nibble first)."""
+        check(self.lib.puter_hip_dequant4(_ptr(dst), _ptr(src), pairCount, config.Scale,
+                                          config.ZeroPoint, dstFormat, srcFormat, self.stream()))
+
+    def Quant(self, dst, src, count, config, dstFormat, srcFormat):
+        """quant/ops.go:10-37: Int8 <- F32, round-half-away(src / Scale) + ZeroPoint, saturated."""
+        check(self.lib.puter_hip_quant(_ptr(dst), _ptr(src), count, config.Scale, config.ZeroPoint,
+                                       dstFormat, srcFormat, self.stream()))
 
     # ---- Matmul: device/interface.go:409-415 ----
     def Matmul(self, out, left, right, rows, inner, cols, format):

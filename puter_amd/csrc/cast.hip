@@ -1,4 +1,5 @@
-// dtype casts between f32 and bf16 / f16 / fp8-E4M3FN / fp8-E5M2.
+// dtype casts between f32 and bf16 / f16 / fp8-E4M3FN / fp8-E5M2 (the int8,
+// int4 and f64 pairs are in quant.hip).
 // Reference: convert/bf16_f32.go:11-38, convert/f16_f32.go:10-42,
 // convert/fp8_f32.go:8-65 (slice-to-slice, len(dst) == len(src)).
 //
@@ -141,6 +142,9 @@ static int launch_cast(void *dst, const void *src, int64_t count, hipStream_t st
     return check_launch("cast");
 }
 
+// int8 / int4 / f64 legs (quant.hip)
+int cast_ext(void *dst, int dst_dtype, const void *src, int src_dtype, int64_t count, hipStream_t s);
+
 }  // namespace puter
 
 using namespace puter;
@@ -150,6 +154,8 @@ extern "C" int puter_hip_cast(void *dst, int dst_dtype, const void *src, int src
     if (count < 0) return fail(PUTER_ERR_INVALID, "cast: negative count");
     if (count == 0) return PUTER_OK;
     if (!dst || !src) return fail(PUTER_ERR_NIL, "cast: nil buffer");
+    const auto ext = [](int dt) { return dt == PUTER_I8 || dt == PUTER_I4 || dt == PUTER_F64; };
+    if (ext(dst_dtype) || ext(src_dtype)) return cast_ext(dst, dst_dtype, src, src_dtype, count, as_stream(stream));
     if (!is_float_dtype(dst_dtype) || !is_float_dtype(src_dtype) ||
         (dst_dtype != PUTER_F32 && src_dtype != PUTER_F32))
         return fail(PUTER_ERR_INVALID, "cast: unsupported pair %d -> %d", src_dtype, dst_dtype);

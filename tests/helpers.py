@@ -40,6 +40,8 @@ def to_dev(arr):
     arr = np.ascontiguousarray(arr)
     if arr.dtype == np.uint16:
         t = torch.from_numpy(arr.view(np.int16))
+    elif arr.dtype == np.uint64:
+        t = torch.from_numpy(arr.view(np.int64))
     elif arr.dtype == np.uint8:
         t = torch.from_numpy(arr)
     else:
@@ -50,7 +52,8 @@ def to_dev(arr):
 def empty_dev(shape, np_dtype):
     import torch
     table = {np.float32: torch.float32, np.uint16: torch.int16, np.uint8: torch.uint8,
-             np.int32: torch.int32}
+             np.int32: torch.int32, np.int8: torch.int8, np.float64: torch.float64,
+             np.uint64: torch.int64}
     return torch.empty(tuple(shape), dtype=table[np.dtype(np_dtype).type], device="cuda")
 
 
