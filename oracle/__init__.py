@@ -78,6 +78,7 @@ def lib():
         for name in ("or_dequant_int8", "or_dequant_int4", "or_quant_int8"):
             getattr(_lib, name).argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_float, C.c_int]
         _lib.or_cast_ext.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_size_t]
+        _lib.or_matmul.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 3 + [C.c_int]
         _lib.oracle_set_threads.argtypes = [C.c_int]
         _lib.oracle_get_threads.restype = C.c_int
     return _lib
@@ -360,6 +361,17 @@ def matmul_f32(left, right):
     cols = right.shape[1]
     out = np.empty((rows, cols), np.float32)
     _check(lib().or_matmul_f32(_p(out), _p(left), _p(right), rows, inner, cols), "matmul")
+    return out
+
+
+def matmul(left, right, dtype):
+    """Matmul in F32 / F64 / BF16 / F16 (bf16 and f16 as uint16 bit patterns)."""
+    npt = {F32: np.float32, F64: np.float64, BF16: np.uint16, F16: np.uint16}[dtype]
+    left = _c(left, npt); right = _c(right, npt)
+    rows, inner = left.shape
+    cols = right.shape[1]
+    out = np.empty((rows, cols), npt)
+    _check(lib().or_matmul(_p(out), _p(left), _p(right), rows, inner, cols, dtype), "matmul")
     return out
 
 

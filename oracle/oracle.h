@@ -177,6 +177,8 @@ int or_flash_attention(int causal, const void *query, const void *key, const voi
 /* ---- matmul.c ---- */
 int or_matmul_f32(float *out, const float *left, const float *right,
                   int64_t rows, int64_t inner, int64_t cols);
+int or_matmul(void *out, const void *left, const void *right, int64_t rows, int64_t inner,
+              int64_t cols, int dtype);
 
 #ifdef __cplusplus
 }

@@ -382,7 +382,7 @@ class Backend:
         check(self.lib.puter_hip_quant(_ptr(dst), _ptr(src), count, config.Scale, config.ZeroPoint,
                                        dstFormat, srcFormat, self.stream()))
 
-    # ---- Matmul: device/interface.go:409-415 ----
+    # ---- Matmul: device/interface.go:409-415 (F32, F64, BF16, F16) ----
     def Matmul(self, out, left, right, rows, inner, cols, format):
         check(self.lib.puter_hip_matmul(_ptr(out), _ptr(left), _ptr(right), rows, inner, cols,
                                         format, self.stream()))

@@ -1,12 +1,45 @@
-// f32 Matmul: out[rows, cols] = left[rows, inner] . right[inner, cols], row-major.
-// Reference: device/interface.go:409-415, device/cpu/matmul/compute.go:46-62.
-// Support kernel for the f32 pre-norm attention block (Q/K/V/O projections):
-// 64x64 output tile per 256-thread block, 16-deep K slices staged in LDS, a
-// 4x4 register micro-tile per thread, f32 FMA accumulation.
+// Matmul: out[rows, cols] = left[rows, inner] . right[inner, cols], row-major.
+// Reference: device/interface.go:409-415, device/cpu/matmul/compute.go:46-92
+// (dispatchMatmul: F32, F64, F16, BF16; the 16-bit formats widen to f32, sum in
+// f32 and store the sum rounded to nearest even, compute.go:74-92).
+//
+// bf16 / f16: MFMA GEMM.  A 256-thread block (4 waves, 2 x 2) computes a 256 x 128
+// tile of the output; wave (wm, wn) owns rows 128 wm .. +127 and columns 64 wn ..
+// +63 as 4 x 2 v_mfma_f32_32x32x16 accumulators.  K advances 32 at a time; the
+// A (256 x 32) and B (32 x 128) slices are copied HBM -> LDS by
+// buffer_load ... lds, double buffered, the next slice's copy issued before the
+// current one is computed.  The block computes C^T = B^T . A^T so that a lane's
+// accumulator column is one output row and its registers hold runs of 4
+// consecutive output columns (8-byte stores):
+//   A operand (B^T[n, k]): 8 consecutive k of one column n of the row-major B
+//     slice, read with ds_read_b64_tr_b16 (within a 16-lane group, result lane i
+//     takes element i%4 of the 8 bytes addressed by lane 4j + i/4 as its element
+//     j, so lanes 4j..4j+3 pointing at row k0 + j, columns 4m.. deliver columns
+//     0..15 of rows k0..k0+3 transposed);
+//   B operand (A^T[k, m]): 8 consecutive k of row m of the A slice, one 16-byte
+//     LDS read.
+// LDS layouts: the A slice keeps 64-byte rows with 16-byte chunk c of row r at
+// c ^ (r/4 % 4); the B slice keeps 256-byte rows with chunk c of row r at
+// c ^ 4 (r % 4); both make the operand reads bank-conflict free.  Buffer
+// descriptors end with the matrices, so rows past M (A) or K (B) arrive as
+// zeros; in the last K slice, A chunks past K are given an out-of-range offset
+// and arrive as zeros too (so the garbage of the next row never meets a zero of
+// B: 0 * Inf would be NaN).  Output tiles go to XCDs in 4 x 8 groups (consecutive
+// block ids run round-robin over the 8 XCDs), so the 32 blocks an XCD runs at
+// once share their A and B panels in its L2.
+// Requirements of the MFMA path: N % 8 == 0, K % 8 == 0, 16-byte aligned
+// buffers, 256 * K * 2 and 32 * N * 2 below 2^31; other shapes take the generic
+// kernel (one thread per output, f32 accumulation in index order).
+//
+// f32: 64 x 64 output tile per 256-thread block, 16-deep K slices in LDS, 4 x 4
+// register micro-tile, f32 FMA.  f64: one thread per output, f64 sum in index
+// order (matmulFloat64Scalar, device/cpu/matmul/select_generic.go:39-...).
 #include "common.hpp"
+#include <algorithm>
 
 namespace puter {
 
+// ------------------------------------------------------------------- f32 --
 constexpr int kTile = 64, kDepth = 16;
 
 __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out,
@@ -51,6 +84,238 @@ __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out
         }
 }
 
+// ------------------------------------------------------- generic / f64 --
+template <int DT>
+__global__ __launch_bounds__(256) void matmul_generic_kernel(void *__restrict__ out, const void *__restrict__ A,
+                                                             const void *__restrict__ B, int64_t M, int64_t K,
+                                                             int64_t N) {
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < M * N; idx += (int64_t)gridDim.x * 256) {
+        const int64_t r = idx / N, c = idx - r * N;
+        if constexpr (DT == PUTER_F64) {
+            const double *a = static_cast<const double *>(A) + r * K;
+            const double *b = static_cast<const double *>(B) + c;
+            double s = 0.0;
+            for (int64_t i = 0; i < K; ++i) s += a[i] * b[i * N];
+            static_cast<double *>(out)[idx] = s;
+        } else {
+            using T = typename Elem<DT>::T;
+            const T *a = static_cast<const T *>(A) + r * K;
+            const T *b = static_cast<const T *>(B) + c;
+            float s = 0.0f;
+            for (int64_t i = 0; i < K; ++i) s += Elem<DT>::load(a[i]) * Elem<DT>::load(b[i * N]);
+            static_cast<T *>(out)[idx] = Elem<DT>::store(s);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void matmul_zero_kernel(uint16_t *out, int64_t halves) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < halves; i += (int64_t)gridDim.x * 256) out[i] = 0;
+}
+
+static unsigned generic_blocks(int64_t n) { return (unsigned)std::min<int64_t>((n + 255) / 256, 65536); }
+
+// ------------------------------------------------------------------ MFMA --
+namespace mm {
+constexpr int BM = 256, BN = 128, BK = 32;
+constexpr int A_BYTES = BM * BK * 2;  // 16 KB: 256 rows x 64 bytes
+constexpr int B_BYTES = BK * BN * 2;  // 8 KB: 32 rows x 256 bytes
+constexpr int BUF_WORD3 = 0x00020000; // raw buffer, dword access
+constexpr int OOB = 0x7FFFFFF0;       // an offset past every descriptor's range
+}  // namespace mm
+
+typedef __bf16 mm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mm_f16x8 __attribute__((ext_vector_type(8)));
+typedef short mm_i16x4 __attribute__((ext_vector_type(4)));
+typedef float mm_f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void mm_lds_void;
+typedef __attribute__((address_space(3))) mm_i16x4 mm_lds_i16x4;
+
+struct MmArgs {
+    const uint16_t *a, *b;
+    uint16_t *c;
+    int M, N, K;
+    int tiles_m, tiles_n, groups_m;  // groups_m: 4-tile groups along M
+};
+
+template <int DT>
+__device__ __forceinline__ mm_f32x16 mm_mfma(const mm_i16x4 (&a)[2], const uint4 &b, mm_f32x16 acc) {
+    const uint4 av = __builtin_bit_cast(uint4, __builtin_shufflevector(a[0], a[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    if constexpr (DT == PUTER_BF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mm_bf16x8, av),
+                                                       __builtin_bit_cast(mm_bf16x8, b), acc, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mm_f16x8, av),
+                                                      __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256, 2) void matmul_mfma_kernel(MmArgs p) {
+    using namespace mm;
+    // separate arrays so the compiler can tell the slice being read from the one being copied
+    __shared__ __attribute__((aligned(1024))) char a0s[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char a1s[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char b0s[B_BYTES];
+    __shared__ __attribute__((aligned(1024))) char b1s[B_BYTES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, g = lane >> 5;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // block -> output tile: XCD x runs the 4 x 8 tile groups x, x + 8, ...
+    const int id = blockIdx.x;
+    const int local = id >> 3, grp = (local >> 5) * 8 + (id & 7), w = local & 31;
+    const int tm = (grp % p.groups_m) * 4 + (w & 3);
+    const int tn = (grp / p.groups_m) * 8 + (w >> 2);
+    if (tm >= p.tiles_m || tn >= p.tiles_n) return;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int M = p.M, N = p.N, K = p.K;
+
+    // copy offsets (bytes, relative to the slice's descriptor base)
+    int aoff[4], achunk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // A: wave copies rows 64 w .. +63, 16 per copy, 4 chunks per row
+        const int row = 64 * wave + 16 * i + (lane >> 2);
+        achunk[i] = (lane & 3) ^ ((row >> 2) & 3);
+        aoff[i] = row * K * 2 + achunk[i] * 16;
+    }
+    int boff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // B: wave copies rows 8 w .. +7, 4 per copy, 16 chunks per row
+        const int row = 8 * wave + 4 * i + (lane >> 4);
+        boff[i] = row * N * 2 + (((lane & 15) ^ ((row & 3) << 2)) << 4);
+    }
+    // operand read offsets inside a slice
+    int ard[4][2];  // [mt][k-step]
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const int row = 128 * wm + 32 * mt + l32;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) ard[mt][s] = row * 64 + (((2 * s + g) ^ ((row >> 2) & 3)) << 4);
+    }
+    int brd[2][2];  // [nt][k-step]
+    {
+        const int q = lane >> 4, i = lane & 15, j = i >> 2, m = i & 3;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int nb = 2 * wn + nt;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const int row = 16 * s + 8 * (q >> 1) + j;
+                const int chunk = (4 * nb + 2 * (q & 1) + (m >> 1)) ^ ((row & 3) << 2);
+                brd[nt][s] = row * 256 + (chunk << 4) + 8 * (m & 1);
+            }
+        }
+    }
+
+    const int64_t a_rows_bytes = (int64_t)(M - m0) * K * 2;
+    auto copy_slice = [&](int k0, char *as, char *bs) __attribute__((always_inline)) {
+        const int64_t abase = (int64_t)m0 * K + k0;
+        const int64_t arange = std::min<int64_t>(a_rows_bytes - (int64_t)k0 * 2, OOB);
+        const __amdgpu_buffer_rsrc_t ad = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(p.a + abase), (short)0, (int)arange, BUF_WORD3);
+        const int64_t bbase = (int64_t)k0 * N + n0;
+        const int64_t brange = std::min<int64_t>(((int64_t)K * N - bbase) * 2, OOB);
+        const __amdgpu_buffer_rsrc_t bd = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(p.b + bbase), (short)0, (int)brange, BUF_WORD3);
+        const bool tail = k0 + BK > K;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int off = (tail && k0 + 8 * achunk[i] >= K) ? OOB : aoff[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ad, (mm_lds_void *)(as + (64 * wave + 16 * i) * 64), 16, off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bd, (mm_lds_void *)(bs + (8 * wave + 4 * i) * 256), 16, boff[i], 0, 0, 0);
+    };
+
+    mm_f32x16 acc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = (mm_f32x16){};
+
+    auto compute = [&](const char *as, const char *bs) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            mm_i16x4 bt[2][2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                bt[nt][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bs + brd[nt][s]));
+                bt[nt][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bs + brd[nt][s] + 4 * 256));
+            }
+            uint4 af[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) af[mt] = *reinterpret_cast<const uint4 *>(as + ard[mt][s]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mm_mfma<DT>(bt[nt], af[mt], acc[mt][nt]);
+        }
+    };
+
+    const int nk = (K + BK - 1) / BK;
+    copy_slice(0, a0s, b0s);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    auto slice = [&](int kt, const char *ac, const char *bc, char *an, char *bn) __attribute__((always_inline)) {
+        if (kt + 1 < nk) copy_slice((kt + 1) * BK, an, bn);
+        compute(ac, bc);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's copies of the next slice landed
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        slice(kt, a0s, b0s, a1s, b1s);
+        slice(kt + 1, a1s, b1s, a0s, b0s);
+    }
+    if (kt < nk) slice(kt, a0s, b0s, a1s, b1s);
+
+    // lane holds C[m0 + 128 wm + 32 mt + l32][n0 + 64 wn + 32 nt + 8 (r/4) + 4 g + r%4]
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const int row = m0 + 128 * wm + 32 * mt + l32;
+        if (row >= M) continue;
+        uint16_t *crow = p.c + (int64_t)row * N;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int col = n0 + 64 * wn + 32 * nt + 8 * rb + 4 * g;
+                if (col >= N) continue;
+                uint32_t h[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) h[i] = Elem<DT>::store(acc[mt][nt][4 * rb + i]);
+                *reinterpret_cast<uint2 *>(crow + col) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            }
+    }
+}
+
+template <int DT>
+static int launch_matmul16(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
+                           hipStream_t s) {
+    const bool mfma = N % 8 == 0 && K % 8 == 0 && aligned16(out) && aligned16(left) && aligned16(right) &&
+                      256 * K * 2 < mm::OOB && 32 * N * 2 < mm::OOB && M <= 0x3FFFFFFF && N <= 0x3FFFFFFF;
+    if (mfma) {
+        MmArgs p;
+        p.a = static_cast<const uint16_t *>(left);
+        p.b = static_cast<const uint16_t *>(right);
+        p.c = static_cast<uint16_t *>(out);
+        p.M = (int)M; p.N = (int)N; p.K = (int)K;
+        p.tiles_m = (int)((M + mm::BM - 1) / mm::BM);
+        p.tiles_n = (int)((N + mm::BN - 1) / mm::BN);
+        p.groups_m = (p.tiles_m + 3) / 4;
+        const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
+        const int64_t blocks = (groups + 7) / 8 * 8 * 32;
+        if (blocks <= 0x7FFFFFFF) {
+            matmul_mfma_kernel<DT><<<(unsigned)blocks, 256, 0, s>>>(p);
+            return check_launch("matmul mfma");
+        }
+    }
+    matmul_generic_kernel<DT><<<generic_blocks(M * N), 256, 0, s>>>(out, left, right, M, K, N);
+    return check_launch("matmul");
+}
+
 }  // namespace puter
 
 using namespace puter;
@@ -58,16 +323,28 @@ using namespace puter;
 extern "C" int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,
                                 int64_t inner, int64_t cols, int dtype, void *stream) {
     if (rows < 0 || inner < 0 || cols < 0) return fail(PUTER_ERR_INVALID, "matmul: negative shape");
-    if (dtype != PUTER_F32) return fail(PUTER_ERR_INVALID, "matmul: unsupported dtype %d (F32 only)", dtype);
+    if (dtype != PUTER_F32 && dtype != PUTER_F64 && dtype != PUTER_BF16 && dtype != PUTER_F16)
+        return fail(PUTER_ERR_INVALID, "matmul: unsupported dtype %d", dtype);
     if (rows == 0 || cols == 0) return PUTER_OK;
     if (!out || !left || !right) return fail(PUTER_ERR_NIL, "matmul: nil buffer");
-    if (inner == 0) {
-        hipError_t e = hipMemsetAsync(out, 0, (size_t)(rows * cols) * sizeof(float), as_stream(stream));
-        return e == hipSuccess ? PUTER_OK : fail(PUTER_ERR_LAUNCH, "matmul: %s", hipGetErrorString(e));
+    if (rows * cols > ((int64_t)1 << 40)) return fail(PUTER_ERR_INVALID, "matmul: output too large");
+    hipStream_t s = as_stream(stream);
+    if (inner == 0) {  // empty sums: zeros (a fill kernel, safe under graph capture)
+        const int64_t halves = rows * cols * (dtype == PUTER_F64 ? 4 : dtype == PUTER_F32 ? 2 : 1);
+        matmul_zero_kernel<<<generic_blocks(halves), 256, 0, s>>>(static_cast<uint16_t *>(out), halves);
+        return check_launch("matmul");
+    }
+    switch (dtype) {
+    case PUTER_BF16: return launch_matmul16<PUTER_BF16>(out, left, right, rows, inner, cols, s);
+    case PUTER_F16: return launch_matmul16<PUTER_F16>(out, left, right, rows, inner, cols, s);
+    case PUTER_F64:
+        matmul_generic_kernel<PUTER_F64><<<generic_blocks(rows * cols), 256, 0, s>>>(out, left, right, rows, inner, cols);
+        return check_launch("matmul");
+    default: break;
     }
     const dim3 grid((unsigned)((cols + kTile - 1) / kTile), (unsigned)((rows + kTile - 1) / kTile));
     if (grid.y > 65535) return fail(PUTER_ERR_INVALID, "matmul: too many rows");
-    matmul_f32_kernel<<<grid, 256, 0, as_stream(stream)>>>(static_cast<float *>(out), static_cast<const float *>(left),
-                                                          static_cast<const float *>(right), rows, inner, cols);
+    matmul_f32_kernel<<<grid, 256, 0, s>>>(static_cast<float *>(out), static_cast<const float *>(left),
+                                           static_cast<const float *>(right), rows, inner, cols);
     return check_launch("matmul");
 }

@@ -1,0 +1,67 @@
+"""GPU tier: Matmul in BF16 / F16 (MFMA kernel and its generic fallback), F64 and
+the empty-inner case, against the oracle restatement of
+device/cpu/matmul/compute.go:46-92 through the C ABI."""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import TOL, assert_close, empty_dev, seeded, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+# (rows, inner, cols): MFMA path (cols % 8 == 0, inner % 8 == 0) with ragged
+# tile edges and a K tail, then shapes that take the generic kernel
+SHAPES = [(256, 256, 128), (300, 200, 136), (1, 8, 8), (513, 1032, 264), (128, 512, 512),
+          (1024, 4096, 1024), (7, 13, 5), (65, 64, 130), (33, 12, 40)]
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("rows,inner,cols", SHAPES)
+def test_matmul_16bit(backend, dt, rows, inner, cols):
+    a = O.from_f32(seeded(rows * 7 + inner, (rows, inner)), dt)
+    b = O.from_f32(seeded(cols * 5 + inner, (inner, cols), 0.0, 0.05), dt)
+    ref = O.to_f32(O.matmul(a, b, dt), dt)
+    out = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, dt)
+    got = O.to_f32(to_host(out, np.uint16), dt)
+    # sums over `inner` in another order than the reference's index order: normwise bar
+    assert_close(got, ref, TOL[dt], elem_tol=None, what="matmul %dx%dx%d" % (rows, inner, cols))
+
+
+def test_matmul_k_tail_never_reads_the_next_row(backend):
+    """inner = 40: the last 32-wide K slice holds 8 valid columns; the chunks past
+    inner must arrive as zeros, not as the next row's first elements.  Row 1 of
+    `left` starts with NaN: only output row 1 may be NaN."""
+    rows, inner, cols = 64, 40, 128
+    a32 = seeded(901, (rows, inner))
+    a32[1, 0] = np.nan
+    a = O.from_f32(a32, O.BF16)
+    b = O.from_f32(seeded(902, (inner, cols), 0.0, 0.05), O.BF16)
+    out = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, O.BF16)
+    got = O.to_f32(to_host(out, np.uint16), O.BF16)
+    ref = O.to_f32(O.matmul(a, b, O.BF16), O.BF16)
+    assert np.isnan(got[1]).all() and np.isnan(ref[1]).all()
+    keep = np.ones(rows, bool)
+    keep[1] = False
+    assert np.isfinite(got[keep]).all()
+    assert_close(got[keep], ref[keep], TOL[O.BF16], elem_tol=None, what="k tail")
+
+
+def test_matmul_f64_and_f32(backend):
+    for rows, inner, cols in [(64, 96, 48), (7, 13, 5)]:
+        a = seeded(rows, (rows, inner)).astype(np.float64)
+        b = seeded(cols + 3, (inner, cols)).astype(np.float64)
+        ref = O.matmul(a, b, O.F64)
+        out = empty_dev((rows, cols), np.float64)
+        backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, O.F64)
+        assert np.allclose(to_host(out, np.float64), ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("dt,np_dt", [(O.BF16, np.uint16), (O.F32, np.float32), (O.F64, np.float64)])
+def test_matmul_empty_inner_is_zero(backend, dt, np_dt):
+    rows, cols = 5, 7   # odd element count
+    out = to_dev(np.full((rows, cols), 7, np_dt))
+    dummy = to_dev(np.zeros(8, np_dt))
+    backend.Matmul(out, dummy, dummy, rows, 0, cols, dt)
+    assert not to_host(out, np_dt).any()
