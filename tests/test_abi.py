@@ -105,7 +105,9 @@ def test_attention_validation(lib):
     bad = list(args)
     bad[15] = 3                                                     # fp8 without scales
     assert lib.puter_hip_paged_decode_attention(*bad) == _lib.ERR_NIL
-    assert lib.puter_hip_matmul(FAKE, FAKE, FAKE, 4, 4, 4, 2, None) == _lib.ERR_INVALID
+    # Matmul takes F32 / F64 / BF16 / F16 (compute.go:46-62); fp8 is rejected
+    assert lib.puter_hip_matmul(FAKE, FAKE, FAKE, 4, 4, 4, 3, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_matmul(FAKE, FAKE, FAKE, -1, 4, 4, 2, None) == _lib.ERR_INVALID
 
 
 def test_backend_class_requires_the_library():
