@@ -235,6 +235,25 @@ def decode(torch, be, puter, fp8):
             "decode_sum_ctx": int(ctx.sum())}
 
 
+def matmul_bf16(torch, be, puter):
+    """Matmul in bf16 (f32 accumulation) on the MFMA GEMM: a square 8192^3 and
+    the MLP up-projection shape rows 8192 x inner 4096 x cols 14336."""
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0006)
+    res = {}
+    for name, (M, K, N) in (("8192c", (8192, 8192, 8192)), ("mlp", (8192, 4096, 14336))):
+        a = torch.randn(M * K, device="cuda", generator=gen).to(torch.bfloat16)
+        b = torch.randn(K * N, device="cuda", generator=gen).to(torch.bfloat16)
+        c = torch.empty(M * N, device="cuda", dtype=torch.bfloat16)
+        t = Timer(torch).time(lambda: be.Matmul(c, a, b, M, K, N, puter.BF16), 10, warmup=3)
+        tf = 2.0 * M * K * N / (t * 1e-3) / 1e12
+        res[f"matmul_bf16_{name}_ms"] = round(t, 3)
+        res[f"matmul_bf16_{name}_TFLOPs"] = round(tf, 1)
+        res[f"matmul_bf16_{name}_mfma_frac"] = round(tf / BF16_PEAK_TFLOPS, 4)
+        del a, b, c
+    torch.cuda.empty_cache()
+    return res
+
+
 def block_f32(torch, be, puter):
     """one pre-norm attention block in f32, batch 1, seq 128, hidden
     512, 8 heads x 64: RMSNorm (eps 1e-6, gamma 1+N(0,.02)) -> Q/K/V projections
@@ -459,7 +478,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="norm,rope,prefill,decode,block,cpu,traffic")
+    ap.add_argument("--only", default="norm,rope,prefill,decode,matmul,block,cpu,traffic")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant kernel N times plus a 1 GiB calibration copy")
     args = ap.parse_args()
@@ -494,6 +513,9 @@ def main():
         configs.update(decode(torch, be, puter, False))
         configs.update(decode(torch, be, puter, True))
         log("decode done")
+    if "matmul" in only:
+        configs.update(matmul_bf16(torch, be, puter))
+        log(f"matmul bf16: {configs['matmul_bf16_8192c_TFLOPs']} TFLOP/s at 8192^3")
     if "block" in only:
         configs.update(block_f32(torch, be, puter))
         log(f"block f32: {configs['block_f32_us']} us, err {configs['block_f32_normwise_err']:.2e}")

@@ -39,3 +39,45 @@ def test_prenorm_attention_block_f32(backend):
                                qd, kd, vd, od, S, S, O.F32)
     backend.Matmul(yd, od, wd[3], S, HID, HID, O.F32)
     assert_close(to_host(yd, np.float32), ref, 1e-5, elem_tol=1e-3, what="pre-norm block")
+
+
+@pytest.mark.parametrize("S,HID,H,KV,D", [(128, 512, 8, 8, 64), (256, 512, 4, 2, 128)])
+def test_prenorm_attention_block_bf16(backend, S, HID, H, KV, D):
+    """The same chain in bf16 storage (f32 arithmetic inside each op), the
+    second shape with grouped K/V heads and head dim 128: the projections run
+    on the MFMA Matmul and the attention on the bf16 prefill kernel.  Each op
+    rounds its output to bf16, as the reference's bf16 kernels do, so the
+    chains agree to the bf16 bar."""
+    import puter_amd
+    BF = O.BF16
+    seed = 0x5EED0100 + S
+    KVW = KV * D
+    enc = lambda a: O.from_f32(np.ascontiguousarray(a, np.float32), BF)  # noqa: E731
+    x = enc(O.normal(seed, S * HID).reshape(S, HID))
+    g = enc(O.normal(seed + 1, HID, 1.0, 0.02))
+    wq = enc(O.normal(seed + 2, HID * HID, 0.0, 0.02).reshape(HID, HID))
+    wk = enc(O.normal(seed + 3, HID * KVW, 0.0, 0.02).reshape(HID, KVW))
+    wv = enc(O.normal(seed + 4, HID * KVW, 0.0, 0.02).reshape(HID, KVW))
+    wo = enc(O.normal(seed + 5, HID * HID, 0.0, 0.02).reshape(HID, HID))
+
+    h = O.rmsnorm(x, g, 1e-6, BF)
+    q, k, v = O.matmul(h, wq, BF), O.matmul(h, wk, BF), O.matmul(h, wv, BF)
+    q = O.rope(q.reshape(S, H, D), dtype=BF).reshape(S, HID)
+    k = O.rope(k.reshape(S, KV, D), dtype=BF).reshape(S, KVW)
+    ref = O.matmul(O.mha(q, k, v, H, D, causal=True, kv_heads=KV, dtype=BF), wo, BF)
+
+    xd, gd, wqd, wkd, wvd, wod = (to_dev(a) for a in (x, g, wq, wk, wv, wo))
+    hd, qd, od, yd = (empty_dev((S, HID), np.uint16) for _ in range(4))
+    kd, vd = (empty_dev((S, KVW), np.uint16) for _ in range(2))
+    backend.RMSNorm(puter_amd.RMSNormConfig(1e-6), xd, gd, hd, S, HID, BF)
+    backend.Matmul(qd, hd, wqd, S, HID, HID, BF)
+    backend.Matmul(kd, hd, wkd, S, HID, KVW, BF)
+    backend.Matmul(vd, hd, wvd, S, HID, KVW, BF)
+    rc = puter_amd.RoPEConfig()
+    backend.RoPE(rc, qd, qd, S, H, D, BF)
+    backend.RoPE(rc, kd, kd, S, KV, D, BF)
+    backend.MultiHeadAttention(puter_amd.MultiHeadAttentionConfig(H, D, True, 0, 0.0, KV),
+                               qd, kd, vd, od, S, S, BF)
+    backend.Matmul(yd, od, wod, S, HID, HID, BF)
+    got = O.to_f32(to_host(yd, np.uint16), BF)
+    assert_close(got, O.to_f32(ref, BF), 1e-2, elem_tol=None, what=f"bf16 block S{S} H{HID}")
