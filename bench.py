@@ -249,7 +249,11 @@ def matmul_bf16(torch, be, puter):
         res[f"matmul_bf16_{name}_ms"] = round(t, 3)
         res[f"matmul_bf16_{name}_TFLOPs"] = round(tf, 1)
         res[f"matmul_bf16_{name}_mfma_frac"] = round(tf / BF16_PEAK_TFLOPS, 4)
-        del a, b, c
+        # context, not this library: torch.matmul on the same operands (hipBLASLt)
+        a2, b2 = a.view(M, K), b.view(K, N)
+        t = Timer(torch).time(lambda: torch.matmul(a2, b2), 10, warmup=3)
+        res[f"context_torch_matmul_bf16_{name}_TFLOPs"] = round(2.0 * M * K * N / (t * 1e-3) / 1e12, 1)
+        del a, b, c, a2, b2
     torch.cuda.empty_cache()
     return res
 
@@ -429,6 +433,20 @@ def profile_dominant(torch, be, puter, launches):
         f"({8 * n} B algorithmic each), {launches} x 1 GiB copy")
 
 
+def profile_matmul(torch, be, puter, launches):
+    """Counter-collection workload for the bf16 GEMM: Matmul 8192^3 `launches`
+    times (random normal operands)."""
+    M = K = N = 8192
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0006)
+    a = torch.randn(M * K, device="cuda", generator=gen).to(torch.bfloat16)
+    b = torch.randn(K * N, device="cuda", generator=gen).to(torch.bfloat16)
+    c = torch.empty(M * N, device="cuda", dtype=torch.bfloat16)
+    for _ in range(launches):
+        be.Matmul(c, a, b, M, K, N, puter.BF16)
+    torch.cuda.synchronize()
+    log(f"profile workload done: {launches} x Matmul bf16 {M}x{K}x{N}")
+
+
 def measure_traffic():
     """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
     passes (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) over
@@ -481,6 +499,8 @@ def main():
     ap.add_argument("--only", default="norm,rope,prefill,decode,matmul,block,cpu,traffic")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant kernel N times plus a 1 GiB calibration copy")
+    ap.add_argument("--profile-matmul", type=int, default=0, metavar="N",
+                    help="only run the bf16 Matmul 8192^3 N times (counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -491,6 +511,9 @@ def main():
     be = puter.Backend()
     if args.profile_dominant:
         profile_dominant(torch, be, puter, args.profile_dominant)
+        return
+    if args.profile_matmul:
+        profile_matmul(torch, be, puter, args.profile_matmul)
         return
     only = set(args.only.split(","))
     ms, step_bytes, per, roof = norm_sweep(torch, be, puter, args.steps, args.warmup)

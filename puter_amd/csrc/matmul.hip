@@ -3,14 +3,17 @@
 // (dispatchMatmul: F32, F64, F16, BF16; the 16-bit formats widen to f32, sum in
 // f32 and store the sum rounded to nearest even, compute.go:74-92).
 //
-// bf16 / f16: MFMA GEMM.  A 256-thread block (4 waves, 2 x 2) computes a 256 x 128
-// tile of the output; wave (wm, wn) owns rows 128 wm .. +127 and columns 64 wn ..
-// +63 as 4 x 2 v_mfma_f32_32x32x16 accumulators.  K advances 32 at a time; the
-// A (256 x 32) and B (32 x 128) slices are copied HBM -> LDS by
-// buffer_load ... lds, double buffered, the next slice's copy issued before the
-// current one is computed.  The block computes C^T = B^T . A^T so that a lane's
-// accumulator column is one output row and its registers hold runs of 4
-// consecutive output columns (8-byte stores):
+// bf16 / f16: MFMA GEMM, two tile shapes from one template (NW = waves along N):
+//   NW = 4 (large problems): a 512-thread block (8 waves, 2 x 4) computes a
+//     256 x 256 output tile, K advancing 64 at a time, one block per CU;
+//   NW = 2 (fewer than 256 such tiles): a 256-thread block (4 waves, 2 x 2)
+//     computes a 256 x 128 tile, K advancing 32, two blocks per CU.
+// Wave (wm, wn) owns rows 128 wm .. +127 and columns 64 wn .. +63 as 4 x 2
+// v_mfma_f32_32x32x16 accumulators.  The A (256 x BK) and B (BK x 64 NW)
+// slices are copied HBM -> LDS by buffer_load ... lds, double buffered, the next
+// slice's copy issued before the current one is computed.  The block computes
+// C^T = B^T . A^T so that a lane's accumulator column is one output row and its
+// registers hold runs of 4 consecutive output columns (8-byte stores):
 //   A operand (B^T[n, k]): 8 consecutive k of one column n of the row-major B
 //     slice, read with ds_read_b64_tr_b16 (within a 16-lane group, result lane i
 //     takes element i%4 of the 8 bytes addressed by lane 4j + i/4 as its element
@@ -18,17 +21,17 @@
 //     0..15 of rows k0..k0+3 transposed);
 //   B operand (A^T[k, m]): 8 consecutive k of row m of the A slice, one 16-byte
 //     LDS read.
-// LDS layouts: the A slice keeps 64-byte rows with 16-byte chunk c of row r at
-// c ^ (r/4 % 4); the B slice keeps 256-byte rows with chunk c of row r at
-// c ^ 4 (r % 4); both make the operand reads bank-conflict free.  Buffer
-// descriptors end with the matrices, so rows past M (A) or K (B) arrive as
-// zeros; in the last K slice, A chunks past K are given an out-of-range offset
-// and arrive as zeros too (so the garbage of the next row never meets a zero of
-// B: 0 * Inf would be NaN).  Output tiles go to XCDs in 4 x 8 groups (consecutive
-// block ids run round-robin over the 8 XCDs), so the 32 blocks an XCD runs at
-// once share their A and B panels in its L2.
+// LDS layouts: the A slice keeps rows of 2 BK bytes (8 / NW rows per 256 bytes)
+// with 16-byte chunk c of row r at c ^ ((r / (8 / NW)) % 2 NW); the B slice keeps
+// rows of 128 NW bytes with chunk c of row r at c ^ 4 (r % 4); both make the
+// operand reads bank-conflict free.  Buffer descriptors end with the matrices,
+// so rows past M (A) or K (B) arrive as zeros; in the last K slice, A chunks past
+// K are given an out-of-range offset and arrive as zeros too (so the garbage of
+// the next row never meets a zero of B: 0 * Inf would be NaN).  Output tiles go
+// to XCDs in 4 x 8 groups (consecutive block ids run round-robin over the 8
+// XCDs), so the blocks an XCD runs at once share their A and B panels in its L2.
 // Requirements of the MFMA path: N % 8 == 0, K % 8 == 0, 16-byte aligned
-// buffers, 256 * K * 2 and 32 * N * 2 below 2^31; other shapes take the generic
+// buffers, 256 * K * 2 and BK * N * 2 below 2^31; other shapes take the generic
 // kernel (one thread per output, f32 accumulation in index order).
 //
 // f32: 64 x 64 output tile per 256-thread block, 16-deep K slices in LDS, 4 x 4
@@ -116,9 +119,7 @@ static unsigned generic_blocks(int64_t n) { return (unsigned)std::min<int64_t>((
 
 // ------------------------------------------------------------------ MFMA --
 namespace mm {
-constexpr int BM = 256, BN = 128, BK = 32;
-constexpr int A_BYTES = BM * BK * 2;  // 16 KB: 256 rows x 64 bytes
-constexpr int B_BYTES = BK * BN * 2;  // 8 KB: 32 rows x 256 bytes
+constexpr int BM = 256;
 constexpr int BUF_WORD3 = 0x00020000; // raw buffer, dword access
 constexpr int OOB = 0x7FFFFFF0;       // an offset past every descriptor's range
 }  // namespace mm
@@ -148,9 +149,12 @@ __device__ __forceinline__ mm_f32x16 mm_mfma(const mm_i16x4 (&a)[2], const uint4
                                                       __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
 }
 
-template <int DT>
-__global__ __launch_bounds__(256, 2) void matmul_mfma_kernel(MmArgs p) {
+template <int DT, int NW>
+__global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(MmArgs p) {
     using namespace mm;
+    constexpr int BN = 64 * NW, BK = 16 * NW;
+    constexpr int RA = 2 * BK, RB = 2 * BN;            // LDS row bytes of the A and B slices
+    constexpr int A_BYTES = BM * RA, B_BYTES = BK * RB;
     // separate arrays so the compiler can tell the slice being read from the one being copied
     __shared__ __attribute__((aligned(1024))) char a0s[A_BYTES];
     __shared__ __attribute__((aligned(1024))) char a1s[A_BYTES];
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(256, 2) void matmul_mfma_kernel(MmArgs p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, g = lane >> 5;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / NW, wn = wave % NW;
 
     // block -> output tile: XCD x runs the 4 x 8 tile groups x, x + 8, ...
     const int id = blockIdx.x;
@@ -171,40 +175,38 @@ __global__ __launch_bounds__(256, 2) void matmul_mfma_kernel(MmArgs p) {
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.M, N = p.N, K = p.K;
 
-    // copy offsets (bytes, relative to the slice's descriptor base)
+    // copy offsets (bytes, relative to the slice's descriptor base).  A: each copy
+    // moves 1 KB = 32 / NW rows of 2 NW chunks, 4 copies per wave.
     int aoff[4], achunk[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {  // A: wave copies rows 64 w .. +63, 16 per copy, 4 chunks per row
-        const int row = 64 * wave + 16 * i + (lane >> 2);
-        achunk[i] = (lane & 3) ^ ((row >> 2) & 3);
+    for (int i = 0; i < 4; ++i) {
+        const int row = (128 / NW) * wave + (32 / NW) * i + lane / (2 * NW);
+        achunk[i] = (lane % (2 * NW)) ^ ((row / (8 / NW)) % (2 * NW));
         aoff[i] = row * K * 2 + achunk[i] * 16;
     }
-    int boff[2];
+    // B: each copy moves 8 / NW rows of 8 NW chunks; wave w copies rows 8 w .. +7
+    int boff[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {  // B: wave copies rows 8 w .. +7, 4 per copy, 16 chunks per row
-        const int row = 8 * wave + 4 * i + (lane >> 4);
-        boff[i] = row * N * 2 + (((lane & 15) ^ ((row & 3) << 2)) << 4);
+    for (int i = 0; i < NW; ++i) {
+        const int row = 8 * wave + (8 / NW) * i + lane / (8 * NW);
+        boff[i] = row * N * 2 + (((lane % (8 * NW)) ^ ((row & 3) << 2)) << 4);
     }
-    // operand read offsets inside a slice
-    int ard[4][2];  // [mt][k-step]
+    // operand read offsets inside a slice: A row 128 wm + 32 mt + l32 at k-step s
+    // (chunk 2 s + g; the swizzle depends on l32 only), B rows 16 s + ...
+    int ard[NW];
+    {
+        const int sw = (l32 / (8 / NW)) % (2 * NW);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const int row = 128 * wm + 32 * mt + l32;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) ard[mt][s] = row * 64 + (((2 * s + g) ^ ((row >> 2) & 3)) << 4);
+        for (int s = 0; s < NW; ++s) ard[s] = (128 * wm + l32) * RA + (((2 * s + g) ^ sw) << 4);
     }
-    int brd[2][2];  // [nt][k-step]
+    int brd[2];
     {
         const int q = lane >> 4, i = lane & 15, j = i >> 2, m = i & 3;
+        const int row = 8 * (q >> 1) + j;
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const int nb = 2 * wn + nt;
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const int row = 16 * s + 8 * (q >> 1) + j;
-                const int chunk = (4 * nb + 2 * (q & 1) + (m >> 1)) ^ ((row & 3) << 2);
-                brd[nt][s] = row * 256 + (chunk << 4) + 8 * (m & 1);
-            }
+            const int chunk = (4 * (2 * wn + nt) + 2 * (q & 1) + (m >> 1)) ^ ((row & 3) << 2);
+            brd[nt] = row * RB + (chunk << 4) + 8 * (m & 1);
         }
     }
 
@@ -222,11 +224,15 @@ __global__ __launch_bounds__(256, 2) void matmul_mfma_kernel(MmArgs p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int off = (tail && k0 + 8 * achunk[i] >= K) ? OOB : aoff[i];
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ad, (mm_lds_void *)(as + (64 * wave + 16 * i) * 64), 16, off, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ad, (mm_lds_void *)(as + ((128 / NW) * wave + (32 / NW) * i) * RA), 16, off, 0, 0, 0);
         }
+        // (a constant trip count: a loop bound that depends on NW loses the kernel's host stub)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(bd, (mm_lds_void *)(bs + (8 * wave + 4 * i) * 256), 16, boff[i], 0, 0, 0);
+        for (int i = 0; i < 4; ++i)
+            if (i < NW)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    bd, (mm_lds_void *)(bs + (8 * wave + (8 / NW) * i) * RB), 16, boff[i], 0, 0, 0);
     };
 
     mm_f32x16 acc[4][2];
@@ -237,16 +243,17 @@ __global__ __launch_bounds__(256, 2) void matmul_mfma_kernel(MmArgs p) {
 
     auto compute = [&](const char *as, const char *bs) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < NW; ++s) {
             mm_i16x4 bt[2][2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                bt[nt][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bs + brd[nt][s]));
-                bt[nt][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bs + brd[nt][s] + 4 * 256));
+                const char *bp = bs + brd[nt] + s * 16 * RB;
+                bt[nt][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)bp);
+                bt[nt][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bp + 4 * RB));
             }
             uint4 af[4];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) af[mt] = *reinterpret_cast<const uint4 *>(as + ard[mt][s]);
+            for (int mt = 0; mt < 4; ++mt) af[mt] = *reinterpret_cast<const uint4 *>(as + ard[s] + mt * 32 * RA);
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -291,26 +298,35 @@ __global__ __launch_bounds__(256, 2) void matmul_mfma_kernel(MmArgs p) {
     }
 }
 
+// Launches the NW-wide MFMA kernel; returns 1 when the shape does not fit it.
+template <int DT, int NW>
+static int launch_mfma(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
+                       hipStream_t s) {
+    if (256 * K * 2 >= mm::OOB || 16 * NW * N * 2 >= mm::OOB || M > 0x3FFFFFFF || N > 0x3FFFFFFF) return 1;
+    MmArgs p;
+    p.a = static_cast<const uint16_t *>(left);
+    p.b = static_cast<const uint16_t *>(right);
+    p.c = static_cast<uint16_t *>(out);
+    p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    p.tiles_m = (int)((M + mm::BM - 1) / mm::BM);
+    p.tiles_n = (int)((N + 64 * NW - 1) / (64 * NW));
+    p.groups_m = (p.tiles_m + 3) / 4;
+    const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
+    const int64_t blocks = (groups + 7) / 8 * 8 * 32;
+    if (blocks > 0x7FFFFFFF) return 1;
+    matmul_mfma_kernel<DT, NW><<<(unsigned)blocks, 128 * NW, 0, s>>>(p);
+    return 0;
+}
+
 template <int DT>
 static int launch_matmul16(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
                            hipStream_t s) {
-    const bool mfma = N % 8 == 0 && K % 8 == 0 && aligned16(out) && aligned16(left) && aligned16(right) &&
-                      256 * K * 2 < mm::OOB && 32 * N * 2 < mm::OOB && M <= 0x3FFFFFFF && N <= 0x3FFFFFFF;
-    if (mfma) {
-        MmArgs p;
-        p.a = static_cast<const uint16_t *>(left);
-        p.b = static_cast<const uint16_t *>(right);
-        p.c = static_cast<uint16_t *>(out);
-        p.M = (int)M; p.N = (int)N; p.K = (int)K;
-        p.tiles_m = (int)((M + mm::BM - 1) / mm::BM);
-        p.tiles_n = (int)((N + mm::BN - 1) / mm::BN);
-        p.groups_m = (p.tiles_m + 3) / 4;
-        const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
-        const int64_t blocks = (groups + 7) / 8 * 8 * 32;
-        if (blocks <= 0x7FFFFFFF) {
-            matmul_mfma_kernel<DT><<<(unsigned)blocks, 256, 0, s>>>(p);
-            return check_launch("matmul mfma");
-        }
+    if (N % 8 == 0 && K % 8 == 0 && aligned16(out) && aligned16(left) && aligned16(right)) {
+        // 256 x 256 tiles once they fill every CU, else 256 x 128 at two blocks per CU
+        const int64_t wide_tiles = ((M + 255) / 256) * ((N + 255) / 256);
+        const int rc = wide_tiles >= 256 ? launch_mfma<DT, 4>(out, left, right, M, K, N, s)
+                                         : launch_mfma<DT, 2>(out, left, right, M, K, N, s);
+        if (rc == 0) return check_launch("matmul mfma");
     }
     matmul_generic_kernel<DT><<<generic_blocks(M * N), 256, 0, s>>>(out, left, right, M, K, N);
     return check_launch("matmul");

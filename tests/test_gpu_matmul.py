@@ -28,6 +28,27 @@ def test_matmul_16bit(backend, dt, rows, inner, cols):
     assert_close(got, ref, TOL[dt], elem_tol=None, what="matmul %dx%dx%d" % (rows, inner, cols))
 
 
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("rows,inner,cols", [(4000, 200, 4104), (4096, 1024, 4096)])
+def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
+    """Shapes with at least 256 output tiles of 256 x 256 take the 8-wave kernel
+    (64-deep K slices): the first with ragged rows, columns and a K tail.  The
+    oracle checks one row in every 256-row band (all columns, so every tile) and
+    the last row; the whole product is checked against numpy's f64 product of
+    the same 16-bit inputs."""
+    a = O.from_f32(seeded(rows + 11 * inner, (rows, inner)), dt)
+    b = O.from_f32(seeded(cols + 13 * inner, (inner, cols), 0.0, 0.05), dt)
+    out = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, dt)
+    got = O.to_f32(to_host(out, np.uint16), dt)
+    sample = sorted({t * 256 + (t * 37) % 256 for t in range((rows + 255) // 256) if t * 256 + (t * 37) % 256 < rows}
+                    | {rows - 1})
+    ref = O.to_f32(O.matmul(np.ascontiguousarray(a[sample]), b, dt), dt)
+    assert_close(got[sample], ref, TOL[dt], elem_tol=None, what="wide matmul rows %s" % sample[:4])
+    full = O.to_f32(a, dt).astype(np.float64) @ O.to_f32(b, dt).astype(np.float64)
+    assert_close(got, full, TOL[dt], elem_tol=None, what="wide matmul %dx%dx%d" % (rows, inner, cols))
+
+
 def test_matmul_k_tail_never_reads_the_next_row(backend):
     """inner = 40: the last 32-wide K slice holds 8 valid columns; the chunks past
     inner must arrive as zeros, not as the next row's first elements.  Row 1 of
@@ -46,6 +67,26 @@ def test_matmul_k_tail_never_reads_the_next_row(backend):
     keep[1] = False
     assert np.isfinite(got[keep]).all()
     assert_close(got[keep], ref[keep], TOL[O.BF16], elem_tol=None, what="k tail")
+
+
+def test_matmul_wide_k_tail_never_reads_the_next_row(backend):
+    """The same isolation on the 8-wave kernel: inner = 72 leaves 8 valid columns
+    in the last 64-wide slice; only output row 1 may be NaN."""
+    rows, inner, cols = 4096, 72, 4096
+    a32 = seeded(903, (rows, inner))
+    a32[1, 0] = np.nan
+    a = O.from_f32(a32, O.BF16)
+    b = O.from_f32(seeded(904, (inner, cols), 0.0, 0.05), O.BF16)
+    out = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, O.BF16)
+    got = O.to_f32(to_host(out, np.uint16), O.BF16)
+    assert np.isnan(got[1]).all()
+    keep = np.ones(rows, bool)
+    keep[1] = False
+    assert np.isfinite(got[keep]).all()
+    sample = [0, 2, 255, 256, 2047, 4095]
+    ref = O.to_f32(O.matmul(np.ascontiguousarray(a[sample]), b, O.BF16), O.BF16)
+    assert_close(got[sample], ref, TOL[O.BF16], elem_tol=None, what="wide k tail")
 
 
 def test_matmul_f64_and_f32(backend):
