@@ -267,6 +267,9 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
     __syncthreads();
     auto slice = [&](int kt, const char *ac, const char *bc, char *an, char *bn) __attribute__((always_inline)) {
         if (kt + 1 < nk) copy_slice((kt + 1) * BK, an, bn);
+        // keep the copies ahead of the compute: left alone, the scheduler sinks them
+        // to the end of the slice, right before the wait, exposing their latency
+        __builtin_amdgcn_sched_barrier(0);
         compute(ac, bc);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's copies of the next slice landed
         __syncthreads();
