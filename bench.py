@@ -236,8 +236,9 @@ def decode(torch, be, puter, fp8):
 
 
 def matmul_bf16(torch, be, puter):
-    """Matmul in bf16 (f32 accumulation) on the MFMA GEMM: a square 8192^3 and
-    the MLP up-projection shape rows 8192 x inner 4096 x cols 14336."""
+    """Matmul in bf16 (f32 accumulation) on the MFMA GEMM: a square 8192^3, the
+    MLP up-projection shape rows 8192 x inner 4096 x cols 14336, and decode-step
+    projections of 64 rows (split-K path)."""
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0006)
     res = {}
     for name, (M, K, N) in (("8192c", (8192, 8192, 8192)), ("mlp", (8192, 4096, 14336))):
@@ -253,6 +254,21 @@ def matmul_bf16(torch, be, puter):
         a2, b2 = a.view(M, K), b.view(K, N)
         t = Timer(torch).time(lambda: torch.matmul(a2, b2), 10, warmup=3)
         res[f"context_torch_matmul_bf16_{name}_TFLOPs"] = round(2.0 * M * K * N / (t * 1e-3) / 1e12, 1)
+        del a, b, c, a2, b2
+    # decode-step projections (batch 64 rows against a weight matrix): HBM-bound,
+    # GB/s of operand + output bytes
+    for M, K, N in ((64, 4096, 4096), (64, 4096, 14336), (64, 14336, 4096)):
+        a = torch.randn(M * K, device="cuda", generator=gen).to(torch.bfloat16)
+        b = torch.randn(K * N, device="cuda", generator=gen).to(torch.bfloat16)
+        c = torch.empty(M * N, device="cuda", dtype=torch.bfloat16)
+        t = Timer(torch).time(lambda: be.Matmul(c, a, b, M, K, N, puter.BF16), 20, warmup=3)
+        name = f"matmul_bf16_m{M}_k{K}_n{N}"
+        byt = 2 * (M * K + K * N + M * N)
+        res[f"{name}_us"] = round(t * 1e3, 1)
+        res[f"{name}_GBs"] = round(byt / (t * 1e-3) / 1e9, 1)
+        a2, b2 = a.view(M, K), b.view(K, N)
+        t = Timer(torch).time(lambda: torch.matmul(a2, b2), 20, warmup=3)
+        res[f"context_torch_{name}_us"] = round(t * 1e3, 1)
         del a, b, c, a2, b2
     torch.cuda.empty_cache()
     return res

@@ -10,8 +10,9 @@
 //     computes a 256 x 128 tile, K advancing 32, two blocks per CU.
 // Wave (wm, wn) owns rows 128 wm .. +127 and columns 64 wn .. +63 as 4 x 2
 // v_mfma_f32_32x32x16 accumulators.  The A (256 x BK) and B (BK x 64 NW)
-// slices are copied HBM -> LDS by buffer_load ... lds, double buffered, the next
-// slice's copy issued before the current one is computed.  The block computes
+// slices are copied HBM -> LDS by buffer_load ... lds, double buffered (NW = 4)
+// or on a 3-stage ring (NW = 2), each slice's copies issued before the slice
+// ahead of it is computed.  The block computes
 // C^T = B^T . A^T so that a lane's accumulator column is one output row and its
 // registers hold runs of 4 consecutive output columns (8-byte stores):
 //   A operand (B^T[n, k]): 8 consecutive k of one column n of the row-major B
@@ -39,6 +40,8 @@
 // order (matmulFloat64Scalar, device/cpu/matmul/select_generic.go:39-...).
 #include "common.hpp"
 #include <algorithm>
+#include <cstdint>
+#include <mutex>
 
 namespace puter {
 
@@ -149,17 +152,26 @@ __device__ __forceinline__ mm_f32x16 mm_mfma(const mm_i16x4 (&a)[2], const uint4
                                                       __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
 }
 
-template <int DT, int NW>
+template <int DT, int NW, int BK, int S>
 __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(MmArgs p) {
     using namespace mm;
-    constexpr int BN = 64 * NW, BK = 16 * NW;
+    constexpr int BN = 64 * NW;
     constexpr int RA = 2 * BK, RB = 2 * BN;            // LDS row bytes of the A and B slices
     constexpr int A_BYTES = BM * RA, B_BYTES = BK * RB;
-    // separate arrays so the compiler can tell the slice being read from the one being copied
-    __shared__ __attribute__((aligned(1024))) char a0s[A_BYTES];
-    __shared__ __attribute__((aligned(1024))) char a1s[A_BYTES];
-    __shared__ __attribute__((aligned(1024))) char b0s[B_BYTES];
-    __shared__ __attribute__((aligned(1024))) char b1s[B_BYTES];
+    constexpr int AC = RA / 16;                         // 16-byte chunks per A row
+    constexpr int APW = RA / 4 / (2 * NW);              // A copies per wave per slice
+    constexpr int BPW = BK / 16;                        // B copies per wave per slice
+    constexpr int KS = BK / 16;                         // k-steps per slice
+    // a ring of S slices in separate arrays, so the compiler can tell the slice being
+    // read from the ones being copied (unused ring positions shrink to 16 bytes)
+    __shared__ __attribute__((aligned(1024))) char as0[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char as1[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char as2[S > 2 ? A_BYTES : 16];
+    __shared__ __attribute__((aligned(1024))) char as3[S > 3 ? A_BYTES : 16];
+    __shared__ __attribute__((aligned(1024))) char bs0[B_BYTES];
+    __shared__ __attribute__((aligned(1024))) char bs1[B_BYTES];
+    __shared__ __attribute__((aligned(1024))) char bs2[S > 2 ? B_BYTES : 16];
+    __shared__ __attribute__((aligned(1024))) char bs3[S > 3 ? B_BYTES : 16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -176,28 +188,27 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
     const int M = p.M, N = p.N, K = p.K;
 
     // copy offsets (bytes, relative to the slice's descriptor base).  A: each copy
-    // moves 1 KB = 32 / NW rows of 2 NW chunks, 4 copies per wave.
+    // moves 1 KB = 1024 / RA rows of AC chunks; B: 1024 / RB rows of RB / 16 chunks
     int aoff[4], achunk[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = (128 / NW) * wave + (32 / NW) * i + lane / (2 * NW);
-        achunk[i] = (lane % (2 * NW)) ^ ((row / (8 / NW)) % (2 * NW));
+    for (int i = 0; i < APW; ++i) {
+        const int row = (BM / (2 * NW)) * wave + (1024 / RA) * i + lane / AC;
+        achunk[i] = (lane % AC) ^ ((row / (256 / RA)) % AC);
         aoff[i] = row * K * 2 + achunk[i] * 16;
     }
-    // B: each copy moves 8 / NW rows of 8 NW chunks; wave w copies rows 8 w .. +7
     int boff[4];
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
-        const int row = 8 * wave + (8 / NW) * i + lane / (8 * NW);
-        boff[i] = row * N * 2 + (((lane % (8 * NW)) ^ ((row & 3) << 2)) << 4);
+    for (int i = 0; i < BPW; ++i) {
+        const int row = (BK / (2 * NW)) * wave + (1024 / RB) * i + lane / (RB / 16);
+        boff[i] = row * N * 2 + (((lane % (RB / 16)) ^ ((row & 3) << 2)) << 4);
     }
-    // operand read offsets inside a slice: A row 128 wm + 32 mt + l32 at k-step s
-    // (chunk 2 s + g; the swizzle depends on l32 only), B rows 16 s + ...
-    int ard[NW];
+    // operand reads: A row 128 wm + 32 mt + l32 at k-step s is chunk 2 s + g (the
+    // swizzle depends on l32 only); B rows 16 s + 8 (q / 2) + j (+4 for the second half)
+    int ard[4];
     {
-        const int sw = (l32 / (8 / NW)) % (2 * NW);
+        const int sw = (l32 / (256 / RA)) % AC;
 #pragma unroll
-        for (int s = 0; s < NW; ++s) ard[s] = (128 * wm + l32) * RA + (((2 * s + g) ^ sw) << 4);
+        for (int s = 0; s < KS; ++s) ard[s] = (128 * wm + l32) * RA + (((2 * s + g) ^ sw) << 4);
     }
     int brd[2];
     {
@@ -221,18 +232,20 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
         const __amdgpu_buffer_rsrc_t bd = __builtin_amdgcn_make_buffer_rsrc(
             (void *)(p.b + bbase), (short)0, (int)brange, BUF_WORD3);
         const bool tail = k0 + BK > K;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int off = (tail && k0 + 8 * achunk[i] >= K) ? OOB : aoff[i];
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ad, (mm_lds_void *)(as + ((128 / NW) * wave + (32 / NW) * i) * RA), 16, off, 0, 0, 0);
-        }
-        // (a constant trip count: a loop bound that depends on NW loses the kernel's host stub)
+        // (constant trip counts: a loop bound that depends on the template arguments
+        // loses the kernel's host stub)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            if (i < NW)
+            if (i < APW) {
+                const int off = (tail && k0 + 8 * achunk[i] >= K) ? OOB : aoff[i];
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    bd, (mm_lds_void *)(bs + (8 * wave + (8 / NW) * i) * RB), 16, boff[i], 0, 0, 0);
+                    ad, (mm_lds_void *)(as + ((BM / (2 * NW)) * wave + (1024 / RA) * i) * RA), 16, off, 0, 0, 0);
+            }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < BPW)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    bd, (mm_lds_void *)(bs + ((BK / (2 * NW)) * wave + (1024 / RB) * i) * RB), 16, boff[i], 0, 0, 0);
     };
 
     mm_f32x16 acc[4][2];
@@ -243,7 +256,8 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
 
     auto compute = [&](const char *as, const char *bs) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < NW; ++s) {
+        for (int s = 0; s < 4; ++s) {
+            if (s >= KS) break;
             mm_i16x4 bt[2][2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
@@ -262,24 +276,40 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
     };
 
     const int nk = (K + BK - 1) / BK;
-    copy_slice(0, a0s, b0s);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    char *const abuf[4] = {as0, as1, as2, as3};
+    char *const bbuf[4] = {bs0, bs1, bs2, bs3};
+    // prologue: slices 0 .. S-2 in flight, slice 0 landed
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i)
+        if (i < nk) copy_slice(i * BK, abuf[i], bbuf[i]);
+    if (S == 2 || nk < 2) __builtin_amdgcn_s_waitcnt(0x0F70);
+    else if (S == 3) __builtin_amdgcn_s_waitcnt(0x0F70 | (APW + BPW));            // vmcnt(one slice)
+    else if (nk < 3) __builtin_amdgcn_s_waitcnt(0x0F70 | (APW + BPW));
+    else __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (APW + BPW)));
     __syncthreads();
-    auto slice = [&](int kt, const char *ac, const char *bc, char *an, char *bn) __attribute__((always_inline)) {
-        if (kt + 1 < nk) copy_slice((kt + 1) * BK, an, bn);
+    // slice kt: issue slice kt + S - 1 into the buffer slice kt - 1 used, compute kt,
+    // wait for slice kt + 1
+    auto slice = [&](int kt, int pos) __attribute__((always_inline)) {
+        const int nxt = kt + S - 1;
+        if (nxt < nk) copy_slice(nxt * BK, abuf[(pos + S - 1) % S], bbuf[(pos + S - 1) % S]);
         // keep the copies ahead of the compute: left alone, the scheduler sinks them
         // to the end of the slice, right before the wait, exposing their latency
         __builtin_amdgcn_sched_barrier(0);
-        compute(ac, bc);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's copies of the next slice landed
+        compute(abuf[pos], bbuf[pos]);
+        const int pending = std::min(nk - 1, nxt) - (kt + 1);   // slices after kt + 1 in flight
+        if (S == 2 || pending <= 0) __builtin_amdgcn_s_waitcnt(0x0F70);
+        else if (pending == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | (APW + BPW));
+        else __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * (APW + BPW)));
         __syncthreads();
     };
     int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        slice(kt, a0s, b0s, a1s, b1s);
-        slice(kt + 1, a1s, b1s, a0s, b0s);
+    for (; kt + S <= nk; kt += S) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) slice(kt + i, i);
     }
-    if (kt < nk) slice(kt, a0s, b0s, a1s, b1s);
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+        if (kt + i < nk) slice(kt + i, i);
 
     // lane holds C[m0 + 128 wm + 32 mt + l32][n0 + 64 wn + 32 nt + 8 (r/4) + 4 g + r%4]
 #pragma unroll
@@ -301,11 +331,13 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
     }
 }
 
-// Launches the NW-wide MFMA kernel; returns 1 when the shape does not fit it.
+// Launches the NW-wide MFMA kernel (NW = 4: 64-deep slices, 2 stages; NW = 2:
+// 32-deep slices on a 3-stage ring); returns 1 when the shape does not fit it.
 template <int DT, int NW>
 static int launch_mfma(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
                        hipStream_t s) {
-    if (256 * K * 2 >= mm::OOB || 16 * NW * N * 2 >= mm::OOB || M > 0x3FFFFFFF || N > 0x3FFFFFFF) return 1;
+    constexpr int BK = NW == 4 ? 64 : 32, S = NW == 4 ? 2 : 3;
+    if (256 * K * 2 >= mm::OOB || BK * N * 2 >= mm::OOB || M > 0x3FFFFFFF || N > 0x3FFFFFFF) return 1;
     MmArgs p;
     p.a = static_cast<const uint16_t *>(left);
     p.b = static_cast<const uint16_t *>(right);
@@ -317,14 +349,247 @@ static int launch_mfma(void *out, const void *left, const void *right, int64_t M
     const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
     const int64_t blocks = (groups + 7) / 8 * 8 * 32;
     if (blocks > 0x7FFFFFFF) return 1;
-    matmul_mfma_kernel<DT, NW><<<(unsigned)blocks, 128 * NW, 0, s>>>(p);
+    matmul_mfma_kernel<DT, NW, BK, S><<<(unsigned)blocks, 128 * NW, 0, s>>>(p);
     return 0;
+}
+
+// ---------------------------------------------------------- skinny (M <= 256) --
+// Decode-time projections (a few rows against a large weight matrix) are bound by
+// streaming `right` once.  A 256-thread block computes a 64 x 128 tile over one
+// chunk of K (split K, ~512 blocks in all), copying 64-deep slices HBM -> LDS on a
+// 3-stage ring (two slices in flight per block, two blocks per CU); wave w owns
+// columns 32 w .. +31 as 2 accumulators (rows 0..31, 32..63).  LDS layouts: A rows
+// of 128 bytes, chunk c of row r at c ^ (r/2 % 8); B rows of 256 bytes, chunk c at
+// c ^ 4 (r % 4).  With more than one chunk, each block writes its f32 partial tile to
+// a scratch buffer and matmul_splitk_reduce_kernel sums the chunks in order (so the
+// result does not depend on scheduling) and rounds once.
+namespace sk {
+constexpr int BM = 64, BN = 128, BK = 64;
+constexpr int RA = 2 * BK, RB = 2 * BN;
+constexpr int A_BYTES = BM * RA, B_BYTES = BK * RB;  // 8 KB, 16 KB
+constexpr int CPW = 6;                               // copies per wave per slice (2 A + 4 B)
+}  // namespace sk
+
+struct SkArgs {
+    const uint16_t *a, *b;
+    uint16_t *c;
+    float *ws;  // [chunks][M][N] partials, or null: store the result
+    int M, N, K, kc;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256, 2) void matmul_skinny_kernel(SkArgs p) {
+    using namespace sk;
+    using mm::OOB;
+    using mm::BUF_WORD3;
+    __shared__ __attribute__((aligned(1024))) char a0s[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char a1s[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char a2s[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char b0s[B_BYTES];
+    __shared__ __attribute__((aligned(1024))) char b1s[B_BYTES];
+    __shared__ __attribute__((aligned(1024))) char b2s[B_BYTES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, g = lane >> 5;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM, kb = blockIdx.z * p.kc;
+    const int M = p.M, N = p.N, K = p.K;
+    const int nk = (min(K, kb + p.kc) - kb + BK - 1) / BK;
+
+    int aoff[2], achunk[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // A: wave copies rows 16 w .. +15, 8 rows per copy
+        const int row = 16 * wave + 8 * i + (lane >> 3);
+        achunk[i] = (lane & 7) ^ ((row >> 1) & 7);
+        aoff[i] = row * K * 2 + achunk[i] * 16;
+    }
+    int boff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // B: wave copies rows 16 w .. +15, 4 rows per copy
+        const int row = 16 * wave + 4 * i + (lane >> 4);
+        boff[i] = row * N * 2 + (((lane & 15) ^ ((row & 3) << 2)) << 4);
+    }
+    int ard[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ard[s] = l32 * RA + (((2 * s + g) ^ ((l32 >> 1) & 7)) << 4);
+    int brd;
+    {
+        const int q = lane >> 4, i = lane & 15, j = i >> 2, m = i & 3;
+        const int row = 8 * (q >> 1) + j;
+        brd = row * RB + (((4 * wave + 2 * (q & 1) + (m >> 1)) ^ ((row & 3) << 2)) << 4) + 8 * (m & 1);
+    }
+
+    const int64_t a_rows_bytes = (int64_t)(M - m0) * K * 2;
+    auto copy_slice = [&](int k0, char *as, char *bs) __attribute__((always_inline)) {
+        const int64_t abase = (int64_t)m0 * K + k0;
+        const int64_t arange = std::min<int64_t>(a_rows_bytes - (int64_t)k0 * 2, OOB);
+        const __amdgpu_buffer_rsrc_t ad = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(p.a + abase), (short)0, (int)arange, BUF_WORD3);
+        const int64_t bbase = (int64_t)k0 * N + n0;
+        const int64_t brange = std::min<int64_t>(((int64_t)K * N - bbase) * 2, OOB);
+        const __amdgpu_buffer_rsrc_t bd = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(p.b + bbase), (short)0, (int)brange, BUF_WORD3);
+        const bool tail = k0 + BK > K;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int off = (tail && k0 + 8 * achunk[i] >= K) ? OOB : aoff[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ad, (mm_lds_void *)(as + (16 * wave + 8 * i) * RA), 16, off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bd, (mm_lds_void *)(bs + (16 * wave + 4 * i) * RB), 16, boff[i], 0, 0, 0);
+    };
+
+    mm_f32x16 acc[2] = {(mm_f32x16){}, (mm_f32x16){}};
+    auto compute = [&](const char *as, const char *bs) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            mm_i16x4 bt[2];
+            bt[0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bs + brd + s * 16 * RB));
+            bt[1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bs + brd + s * 16 * RB + 4 * RB));
+            uint4 af[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) af[mt] = *reinterpret_cast<const uint4 *>(as + ard[s] + mt * 32 * RA);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) acc[mt] = mm_mfma<DT>(bt, af[mt], acc[mt]);
+        }
+    };
+
+    // ring of 3: slice kt lives in buffer kt % 3; slices kt + 1 and kt + 2 are in flight
+    // while kt is computed, and the copy of kt + 2 reuses the buffer kt - 1 finished with
+    copy_slice(kb, a0s, b0s);
+    if (nk > 1) copy_slice(kb + BK, a1s, b1s);
+    if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F70 | CPW);  // vmcnt(6): slice 0 landed
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    auto slice = [&](int kt, const char *ac, const char *bc, char *an, char *bn) __attribute__((always_inline)) {
+        if (kt + 2 < nk) copy_slice(kb + (kt + 2) * BK, an, bn);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ac, bc);
+        if (kt + 2 < nk) __builtin_amdgcn_s_waitcnt(0x0F70 | CPW);  // slice kt + 1 landed
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 3 <= nk; kt += 3) {
+        slice(kt, a0s, b0s, a2s, b2s);
+        slice(kt + 1, a1s, b1s, a0s, b0s);
+        slice(kt + 2, a2s, b2s, a1s, b1s);
+    }
+    if (kt < nk) slice(kt, a0s, b0s, a2s, b2s);
+    if (kt + 1 < nk) slice(kt + 1, a1s, b1s, a0s, b0s);
+
+    // lane holds C[m0 + 32 mt + l32][n0 + 32 wave + 8 (r/4) + 4 g + r%4]
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int row = m0 + 32 * mt + l32;
+        if (row >= M) continue;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int col = n0 + 32 * wave + 8 * rb + 4 * g;
+            if (col >= N) continue;
+            const mm_f32x16 &v = acc[mt];
+            if (p.ws) {
+                float *dst = p.ws + ((int64_t)blockIdx.z * M + row) * N + col;
+                *reinterpret_cast<float4 *>(dst) = make_float4(v[4 * rb], v[4 * rb + 1], v[4 * rb + 2], v[4 * rb + 3]);
+            } else {
+                uint32_t h[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) h[i] = Elem<DT>::store(v[4 * rb + i]);
+                *reinterpret_cast<uint2 *>(p.c + (int64_t)row * N + col) =
+                    make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            }
+        }
+    }
+}
+
+// out = round(sum over chunks z = 0, 1, ... of ws[z]), 4 outputs per thread
+template <int DT>
+__global__ __launch_bounds__(256) void matmul_splitk_reduce_kernel(uint16_t *c, const float *ws, int64_t quads,
+                                                                   int chunks) {
+    const float4 *w4 = reinterpret_cast<const float4 *>(ws);
+    for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < quads; v += (int64_t)gridDim.x * 256) {
+        float4 t = w4[v];
+        for (int z = 1; z < chunks; ++z) {
+            const float4 u = w4[(int64_t)z * quads + v];
+            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+        }
+        const uint32_t h0 = Elem<DT>::store(t.x), h1 = Elem<DT>::store(t.y);
+        const uint32_t h2 = Elem<DT>::store(t.z), h3 = Elem<DT>::store(t.w);
+        reinterpret_cast<uint2 *>(c)[v] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+    }
+}
+
+// Split-K partials live in a stream-ordered pool of the library's own (one per
+// device, created on first use, never trimmed below what it has held), so calls on
+// different streams never share a buffer and no call waits on the host.
+static int scratch_alloc(void **ptr, size_t bytes, hipStream_t s) {
+    static std::mutex mu;
+    static hipMemPool_t pools[64];
+    static bool made[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(PUTER_ERR_UNAVAILABLE, "matmul: no device");
+    hipMemPool_t pool;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!made[dev]) {
+            hipMemPoolProps props = {};
+            props.allocType = hipMemAllocationTypePinned;
+            props.handleTypes = hipMemHandleTypeNone;
+            props.location.type = hipMemLocationTypeDevice;
+            props.location.id = dev;
+            if (hipMemPoolCreate(&pools[dev], &props) != hipSuccess)
+                return fail(PUTER_ERR_UNAVAILABLE, "matmul: cannot create the split-K scratch pool");
+            uint64_t keep = UINT64_MAX;  // (if refused, the pool only returns memory at syncs)
+            (void)hipMemPoolSetAttribute(pools[dev], hipMemPoolAttrReleaseThreshold, &keep);
+            made[dev] = true;
+        }
+        pool = pools[dev];
+    }
+    if (hipMallocFromPoolAsync(ptr, bytes, pool, s) != hipSuccess)
+        return fail(PUTER_ERR_UNAVAILABLE, "matmul: split-K scratch of %zu bytes unavailable", bytes);
+    return PUTER_OK;
+}
+
+// Returns 1 when the shape does not fit the skinny kernel.
+template <int DT>
+static int launch_skinny(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
+                         hipStream_t s) {
+    if (64 * K * 2 >= mm::OOB || sk::BK * N * 2 >= mm::OOB || N > 0x3FFFFFFF) return 1;
+    const int64_t tiles_n = (N + sk::BN - 1) / sk::BN, tiles_m = (M + sk::BM - 1) / sk::BM;
+    if (tiles_n > 0x7FFFFFFF) return 1;
+    const int64_t slices = (K + sk::BK - 1) / sk::BK;
+    int64_t chunks = std::min<int64_t>(std::max<int64_t>((512 + tiles_m * tiles_n - 1) / (tiles_m * tiles_n), 1), slices);
+    chunks = std::min<int64_t>(chunks, 64);
+    const int64_t per = (slices + chunks - 1) / chunks;  // slices per chunk
+    chunks = (slices + per - 1) / per;
+    SkArgs p{static_cast<const uint16_t *>(left), static_cast<const uint16_t *>(right), static_cast<uint16_t *>(out),
+             nullptr, (int)M, (int)N, (int)K, (int)(per * sk::BK)};
+    const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)chunks);
+    if (chunks == 1) {
+        matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
+        return check_launch("matmul skinny");
+    }
+    void *ws = nullptr;
+    if (int rc = scratch_alloc(&ws, (size_t)(chunks * M * N) * sizeof(float), s)) return rc;
+    p.ws = static_cast<float *>(ws);
+    matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
+    const int64_t quads = M * N / 4;
+    matmul_splitk_reduce_kernel<DT><<<(unsigned)std::min<int64_t>((quads + 255) / 256, 4096), 256, 0, s>>>(
+        static_cast<uint16_t *>(out), p.ws, quads, (int)chunks);
+    const int rc = check_launch("matmul split-k");
+    if (hipFreeAsync(ws, s) != hipSuccess && rc == PUTER_OK) return fail(PUTER_ERR_LAUNCH, "matmul: scratch release failed");
+    return rc;
 }
 
 template <int DT>
 static int launch_matmul16(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
                            hipStream_t s) {
     if (N % 8 == 0 && K % 8 == 0 && aligned16(out) && aligned16(left) && aligned16(right)) {
+        if (M <= 256) {
+            const int rc = launch_skinny<DT>(out, left, right, M, K, N, s);
+            if (rc != 1) return rc;
+        }
         // 256 x 256 tiles once they fill every CU, else 256 x 128 at two blocks per CU
         const int64_t wide_tiles = ((M + 255) / 256) * ((N + 255) / 256);
         const int rc = wide_tiles >= 256 ? launch_mfma<DT, 4>(out, left, right, M, K, N, s)

@@ -49,6 +49,50 @@ def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
     assert_close(got, full, TOL[dt], elem_tol=None, what="wide matmul %dx%dx%d" % (rows, inner, cols))
 
 
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("rows,inner,cols", [(64, 4096, 4096), (1, 4104, 2056), (200, 1000, 1024),
+                                             (256, 512, 14336), (3, 64, 8)])
+def test_matmul_16bit_skinny_split_k(backend, dt, rows, inner, cols):
+    """rows <= 256 take the split-K kernel (64 x 128 tiles over chunks of K, f32
+    partials summed in chunk order): ragged rows / columns, K tails, one-chunk and
+    many-chunk splits.  Oracle rows sampled across the tile bands (all columns),
+    numpy's f64 product for the whole output, and two calls bit-identical."""
+    a = O.from_f32(seeded(rows * 3 + inner, (rows, inner)), dt)
+    b = O.from_f32(seeded(cols * 7 + inner, (inner, cols), 0.0, 0.05), dt)
+    ad, bd = to_dev(a), to_dev(b)
+    out = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out, ad, bd, rows, inner, cols, dt)
+    got_bits = to_host(out, np.uint16)
+    got = O.to_f32(got_bits, dt)
+    sample = sorted({0, rows - 1, rows // 2, min(rows - 1, 63), min(rows - 1, 64), min(rows - 1, 131)})
+    ref = O.to_f32(O.matmul(np.ascontiguousarray(a[sample]), b, dt), dt)
+    assert_close(got[sample], ref, TOL[dt], elem_tol=None, what="skinny matmul rows %s" % sample)
+    full = O.to_f32(a, dt).astype(np.float64) @ O.to_f32(b, dt).astype(np.float64)
+    assert_close(got, full, TOL[dt], elem_tol=None, what="skinny matmul %dx%dx%d" % (rows, inner, cols))
+    out2 = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out2, ad, bd, rows, inner, cols, dt)
+    assert np.array_equal(to_host(out2, np.uint16), got_bits)
+
+
+def test_matmul_skinny_k_tail_never_reads_the_next_row(backend):
+    """Split-K path: inner = 72 is two chunks of one 64-deep slice each, the second
+    holding 8 valid columns; only output row 1 may be NaN."""
+    rows, inner, cols = 64, 72, 4096
+    a32 = seeded(905, (rows, inner))
+    a32[1, 0] = np.nan
+    a = O.from_f32(a32, O.BF16)
+    b = O.from_f32(seeded(906, (inner, cols), 0.0, 0.05), O.BF16)
+    out = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, O.BF16)
+    got = O.to_f32(to_host(out, np.uint16), O.BF16)
+    assert np.isnan(got[1]).all()
+    keep = np.ones(rows, bool)
+    keep[1] = False
+    assert np.isfinite(got[keep]).all()
+    ref = O.to_f32(O.matmul(a, b, O.BF16), O.BF16)
+    assert_close(got[keep], ref[keep], TOL[O.BF16], elem_tol=None, what="skinny k tail")
+
+
 def test_matmul_k_tail_never_reads_the_next_row(backend):
     """inner = 40: the last 32-wide K slice holds 8 valid columns; the chunks past
     inner must arrive as zeros, not as the next row's first elements.  Row 1 of
