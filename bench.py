@@ -184,8 +184,26 @@ def prefill(torch, be, puter):
     t = Timer(torch).time(fn, 10, warmup=3)
     flops = 4.0 * B * H * D * S * (S + 1) / 2
     tf = flops / (t * 1e-3) / 1e12
-    return {"prefill_ms": round(t, 3), "prefill_TFLOPs": round(tf, 1),
-            "prefill_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    res = {"prefill_ms": round(t, 3), "prefill_TFLOPs": round(tf, 1),
+           "prefill_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    # context, not this library: torch's flash SDPA backend on the same shape
+    # ([B, H, S, D], K/V heads repeated to 32); null if the backend is unavailable
+    res["context_torch_sdpa_flash_TFLOPs"] = None
+    try:
+        import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        qt = q.view(B, S, H, D).transpose(1, 2).contiguous()
+        kt = k.view(B, S, KV, D).transpose(1, 2).repeat_interleave(H // KV, dim=1).contiguous()
+        vt = v.view(B, S, KV, D).transpose(1, 2).repeat_interleave(H // KV, dim=1).contiguous()
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            t2 = Timer(torch).time(lambda: F.scaled_dot_product_attention(qt, kt, vt, is_causal=True), 10, warmup=3)
+        res["context_torch_sdpa_flash_TFLOPs"] = round(flops / (t2 * 1e-3) / 1e12, 1)
+        del qt, kt, vt
+    except (RuntimeError, ImportError) as ex:
+        log(f"torch flash SDPA unavailable: {ex}")
+    del q, k, v, o
+    torch.cuda.empty_cache()
+    return res
 
 
 def decode(torch, be, puter, fp8):
