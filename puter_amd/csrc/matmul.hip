@@ -356,13 +356,14 @@ static int launch_mfma(void *out, const void *left, const void *right, int64_t M
 // ---------------------------------------------------------- skinny (M <= 256) --
 // Decode-time projections (a few rows against a large weight matrix) are bound by
 // streaming `right` once.  A 256-thread block computes a 64 x 128 tile over one
-// chunk of K (split K, ~512 blocks in all), copying 64-deep slices HBM -> LDS on a
+// chunk of K (split K, at most one wave of 512 blocks when split), copying 64-deep slices HBM -> LDS on a
 // 3-stage ring (two slices in flight per block, two blocks per CU); wave w owns
 // columns 32 w .. +31 as 2 accumulators (rows 0..31, 32..63).  LDS layouts: A rows
 // of 128 bytes, chunk c of row r at c ^ (r/2 % 8); B rows of 256 bytes, chunk c at
 // c ^ 4 (r % 4).  With more than one chunk, each block writes its f32 partial tile to
-// a scratch buffer and matmul_splitk_reduce_kernel sums the chunks in order (so the
-// result does not depend on scheduling) and rounds once.
+// a scratch buffer (the library's, one per device) and matmul_splitk_reduce_kernel
+// sums the chunks in order (so the result does not depend on scheduling) and
+// rounds once.
 namespace sk {
 constexpr int BM = 64, BN = 128, BK = 64;
 constexpr int RA = 2 * BK, RB = 2 * BN;
@@ -520,34 +521,42 @@ __global__ __launch_bounds__(256) void matmul_splitk_reduce_kernel(uint16_t *c, 
     }
 }
 
-// Split-K partials live in a stream-ordered pool of the library's own (one per
-// device, created on first use, never trimmed below what it has held), so calls on
-// different streams never share a buffer and no call waits on the host.
-static int scratch_alloc(void **ptr, size_t bytes, hipStream_t s) {
-    static std::mutex mu;
-    static hipMemPool_t pools[64];
-    static bool made[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(PUTER_ERR_UNAVAILABLE, "matmul: no device");
-    hipMemPool_t pool;
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        if (!made[dev]) {
-            hipMemPoolProps props = {};
-            props.allocType = hipMemAllocationTypePinned;
-            props.handleTypes = hipMemHandleTypeNone;
-            props.location.type = hipMemLocationTypeDevice;
-            props.location.id = dev;
-            if (hipMemPoolCreate(&pools[dev], &props) != hipSuccess)
-                return fail(PUTER_ERR_UNAVAILABLE, "matmul: cannot create the split-K scratch pool");
-            uint64_t keep = UINT64_MAX;  // (if refused, the pool only returns memory at syncs)
-            (void)hipMemPoolSetAttribute(pools[dev], hipMemPoolAttrReleaseThreshold, &keep);
-            made[dev] = true;
+// Split-K partials: one scratch buffer per device, kept for the life of the
+// process and grown on demand.  A call on another stream than the buffer's last
+// user first waits (on the device, hipStreamWaitEvent) for that user's
+// completion event, so calls on different streams never overlap on the buffer
+// and nothing waits on the host except a growth, which lets the last user finish
+// before the old buffer is freed.  The mutex is held from acquisition until the
+// call's launches and event are enqueued.
+struct SplitScratch {
+    std::mutex mu;
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;  // recorded after the last call that used ptr
+    hipStream_t last = nullptr;
+    bool used = false;
+};
+static SplitScratch g_split_scratch[64];
+
+static int scratch_acquire(SplitScratch &sc, size_t need, hipStream_t s) {
+    if (!sc.done && hipEventCreateWithFlags(&sc.done, hipEventDisableTiming) != hipSuccess)
+        return fail(PUTER_ERR_UNAVAILABLE, "matmul: cannot create the split-K event");
+    if (sc.used && sc.last != s && hipStreamWaitEvent(s, sc.done, 0) != hipSuccess)
+        return fail(PUTER_ERR_LAUNCH, "matmul: cannot order the split-K scratch");
+    if (sc.bytes < need) {
+        if (sc.ptr) {
+            if (hipEventSynchronize(sc.done) != hipSuccess || hipFree(sc.ptr) != hipSuccess)
+                return fail(PUTER_ERR_LAUNCH, "matmul: cannot release the split-K scratch");
+            sc.ptr = nullptr;
+            sc.bytes = 0;
         }
-        pool = pools[dev];
+        const size_t grown = (need + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+        if (hipMalloc(&sc.ptr, grown) != hipSuccess) {
+            sc.ptr = nullptr;
+            return fail(PUTER_ERR_UNAVAILABLE, "matmul: split-K scratch of %zu bytes unavailable", grown);
+        }
+        sc.bytes = grown;
     }
-    if (hipMallocFromPoolAsync(ptr, bytes, pool, s) != hipSuccess)
-        return fail(PUTER_ERR_UNAVAILABLE, "matmul: split-K scratch of %zu bytes unavailable", bytes);
     return PUTER_OK;
 }
 
@@ -559,7 +568,9 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
     const int64_t tiles_n = (N + sk::BN - 1) / sk::BN, tiles_m = (M + sk::BM - 1) / sk::BM;
     if (tiles_n > 0x7FFFFFFF) return 1;
     const int64_t slices = (K + sk::BK - 1) / sk::BK;
-    int64_t chunks = std::min<int64_t>(std::max<int64_t>((512 + tiles_m * tiles_n - 1) / (tiles_m * tiles_n), 1), slices);
+    // as many chunks as keep the grid within one wave of 512 blocks (2 per CU): a
+    // partial second wave would run at a fraction of the bandwidth
+    int64_t chunks = std::min<int64_t>(std::max<int64_t>(512 / (tiles_m * tiles_n), 1), slices);
     chunks = std::min<int64_t>(chunks, 64);
     const int64_t per = (slices + chunks - 1) / chunks;  // slices per chunk
     chunks = (slices + per - 1) / per;
@@ -570,15 +581,20 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
         matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
         return check_launch("matmul skinny");
     }
-    void *ws = nullptr;
-    if (int rc = scratch_alloc(&ws, (size_t)(chunks * M * N) * sizeof(float), s)) return rc;
-    p.ws = static_cast<float *>(ws);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(PUTER_ERR_UNAVAILABLE, "matmul: no device");
+    SplitScratch &sc = g_split_scratch[dev];
+    std::lock_guard<std::mutex> lock(sc.mu);
+    if (int rc = scratch_acquire(sc, (size_t)(chunks * M * N) * sizeof(float), s)) return rc;
+    p.ws = static_cast<float *>(sc.ptr);
     matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
     const int64_t quads = M * N / 4;
     matmul_splitk_reduce_kernel<DT><<<(unsigned)std::min<int64_t>((quads + 255) / 256, 4096), 256, 0, s>>>(
         static_cast<uint16_t *>(out), p.ws, quads, (int)chunks);
     const int rc = check_launch("matmul split-k");
-    if (hipFreeAsync(ws, s) != hipSuccess && rc == PUTER_OK) return fail(PUTER_ERR_LAUNCH, "matmul: scratch release failed");
+    if (hipEventRecord(sc.done, s) != hipSuccess) return fail(PUTER_ERR_LAUNCH, "matmul: cannot record the split-K event");
+    sc.last = s;
+    sc.used = true;
     return rc;
 }
 

@@ -74,6 +74,34 @@ def test_matmul_16bit_skinny_split_k(backend, dt, rows, inner, cols):
     assert np.array_equal(to_host(out2, np.uint16), got_bits)
 
 
+def test_matmul_skinny_two_streams_share_the_scratch_safely(backend):
+    """Split-K calls alternate between two streams (the second shape needs a larger
+    scratch than the first, so the buffer grows while the first stream's work may
+    still be queued); every result must match the same call made alone."""
+    import torch
+    shapes = [(64, 4096, 1024), (128, 8192, 2048), (64, 4096, 1024), (32, 2048, 512)]
+    ins = []
+    for i, (m, k, n) in enumerate(shapes):
+        a = O.from_f32(seeded(950 + i, (m, k)), O.BF16)
+        b = O.from_f32(seeded(960 + i, (k, n), 0.0, 0.05), O.BF16)
+        ins.append((to_dev(a), to_dev(b)))
+    alone = []
+    for (m, k, n), (ad, bd) in zip(shapes, ins):
+        out = empty_dev((m, n), np.uint16)
+        backend.Matmul(out, ad, bd, m, k, n, O.BF16)
+        alone.append(to_host(out, np.uint16))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [empty_dev((m, n), np.uint16) for m, k, n in shapes]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, ((m, k, n), (ad, bd)) in enumerate(zip(shapes, ins)):
+            with torch.cuda.stream(streams[i % 2]):
+                backend.Matmul(outs[i], ad, bd, m, k, n, O.BF16)
+        torch.cuda.synchronize()
+        for i in range(len(shapes)):
+            assert np.array_equal(to_host(outs[i], np.uint16), alone[i]), (rep, i)
+
+
 def test_matmul_skinny_k_tail_never_reads_the_next_row(backend):
     """Split-K path: inner = 72 is two chunks of one 64-deep slice each, the second
     holding 8 valid columns; only output row 1 may be NaN."""
