@@ -353,7 +353,7 @@ static int launch_mfma(void *out, const void *left, const void *right, int64_t M
     return 0;
 }
 
-// ---------------------------------------------------------- skinny (M <= 256) --
+// ---------------------------------------------------------- skinny (M <= 512) --
 // Decode-time projections (a few rows against a large weight matrix) are bound by
 // streaming `right` once.  A 256-thread block computes a 64 x 128 tile over one
 // chunk of K (split K, at most one wave of 512 blocks when split), copying 64-deep slices HBM -> LDS on a
@@ -602,7 +602,7 @@ template <int DT>
 static int launch_matmul16(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
                            hipStream_t s) {
     if (N % 8 == 0 && K % 8 == 0 && aligned16(out) && aligned16(left) && aligned16(right)) {
-        if (M <= 256) {
+        if (M <= 512) {
             const int rc = launch_skinny<DT>(out, left, right, M, K, N, s);
             if (rc != 1) return rc;
         }

@@ -51,9 +51,9 @@ def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("rows,inner,cols", [(64, 4096, 4096), (1, 4104, 2056), (200, 1000, 1024),
-                                             (256, 512, 14336), (3, 64, 8)])
+                                             (256, 512, 14336), (3, 64, 8), (500, 1032, 4104)])
 def test_matmul_16bit_skinny_split_k(backend, dt, rows, inner, cols):
-    """rows <= 256 take the split-K kernel (64 x 128 tiles over chunks of K, f32
+    """rows <= 512 take the split-K kernel (64 x 128 tiles over chunks of K, f32
     partials summed in chunk order): ragged rows / columns, K tails, one-chunk and
     many-chunk splits.  Oracle rows sampled across the tile bands (all columns),
     numpy's f64 product for the whole output, and two calls bit-identical."""
