@@ -94,6 +94,16 @@ def norm_sweep(torch, be, puter, steps, warmup):
         per[f"{kind}_{r}x{h}"] = round(8 * r * h / (t * 1e-3) / 1e9, 1)
     dom = [x for x in launches if x[0] == rmax and x[1] == hmax and x[2] == "rms"][0]
     dom_ms = timer.time(dom[3], 50)
+    # context, not this library: the same op in eager torch (h = res + gate * branch,
+    # y = rms_norm(h)), charged the fused op's 8 B/elem
+    r2, b2, h2 = res.view(rmax, hmax), br.view(rmax, hmax), hid.view(rmax, hmax)
+    gate, g2 = mod[2 * hmax:3 * hmax], gamma[:hmax]
+
+    def torch_gr_rms():
+        torch.add(r2, b2 * gate, out=h2)
+        return torch.nn.functional.rms_norm(h2, (hmax,), g2, 1e-5)
+    t_torch = timer.time(torch_gr_rms, 10, warmup=2)
+    per["context_torch_gr_rmsnorm_%dx%d" % (rmax, hmax)] = round(8 * rmax * hmax / (t_torch * 1e-3) / 1e9, 1)
     dom_bytes = 8 * rmax * hmax
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -352,7 +362,7 @@ def block_f32(torch, be, puter):
 
 
 def cpu_configs():
-    """The oracle on bounded samples of configs[2..4], timed on the host cores
+    """The oracle on bounded samples of configs[2..4] and of the bf16 Matmul, timed on the host cores
     (rope and casts are single-threaded in the oracle; SwiGLU, attention rows and
     norms thread over rows)."""
     import numpy as np
@@ -411,6 +421,13 @@ def cpu_configs():
     t = timed(lambda: O.paged_decode(qd, kp, vp, table, ctx, PS, H, KV, D, O.BF16))
     res["cpu_decode_bf16_GBs"] = round(int(ctx.sum()) * KV * D * 2 * 2 / t / 1e9, 3)
     res["cpu_decode_sample"] = f"4 sequences, sum ctx {int(ctx.sum())}"
+    # Matmul bf16: one row of the 8192 x 4096 x 14336 MLP shape (the oracle is one
+    # thread, f32 accumulation in index order)
+    am = O.from_f32(O.normal(31, 4096).reshape(1, 4096), O.BF16)
+    bm = O.from_f32(O.normal(32, 4096 * 14336).reshape(4096, 14336), O.BF16)
+    t = timed(lambda: O.matmul(am, bm, O.BF16))
+    res["cpu_matmul_bf16_TFLOPs"] = round(2.0 * 4096 * 14336 / t / 1e12, 6)
+    res["cpu_matmul_sample"] = "rows 1 x inner 4096 x cols 14336, 1 thread"
     return res
 
 
