@@ -6,7 +6,7 @@
 // bf16 / f16: MFMA GEMM, two tile shapes from one template (NW = waves along N):
 //   NW = 4 (large problems): a 512-thread block (8 waves, 2 x 4) computes a
 //     256 x 256 output tile, K advancing 64 at a time, one block per CU;
-//   NW = 2 (fewer than 256 such tiles): a 256-thread block (4 waves, 2 x 2)
+//   NW = 2 (fewer than 160 such tiles): a 256-thread block (4 waves, 2 x 2)
 //     computes a 256 x 128 tile, K advancing 32, two blocks per CU.
 // Wave (wm, wn) owns rows 128 wm .. +127 and columns 64 wn .. +63 as 4 x 2
 // v_mfma_f32_32x32x16 accumulators.  The A (256 x BK) and B (BK x 64 NW)
@@ -606,9 +606,11 @@ static int launch_matmul16(void *out, const void *left, const void *right, int64
             const int rc = launch_skinny<DT>(out, left, right, M, K, N, s);
             if (rc != 1) return rc;
         }
-        // 256 x 256 tiles once they fill every CU, else 256 x 128 at two blocks per CU
+        // 256 x 256 tiles (one 8-wave block per CU) from 160 such tiles up; below that
+        // 256 x 128 tiles spread over more CUs win (measured: 128 tiles -14% wide,
+        // 168 and more +13-17%)
         const int64_t wide_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-        const int rc = wide_tiles >= 256 ? launch_mfma<DT, 4>(out, left, right, M, K, N, s)
+        const int rc = wide_tiles >= 160 ? launch_mfma<DT, 4>(out, left, right, M, K, N, s)
                                          : launch_mfma<DT, 2>(out, left, right, M, K, N, s);
         if (rc == 0) return check_launch("matmul mfma");
     }
