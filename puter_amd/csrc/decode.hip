@@ -235,12 +235,20 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t keep = ((livev >> (4 * k)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
-            uint4 w;
-            if constexpr (BF) w = vc[k];
-            else w = fp8x8_to_bf16(vc[k]);
-            w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
             float v[8];
-            unpack_vec<PUTER_BF16>(w, v);
+            if constexpr (BF) {
+                uint4 w = vc[k];
+                w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
+                unpack_vec<PUTER_BF16>(w, v);
+            } else {   // E4M3 widened straight to f32 (the same values as through bf16)
+                const uint32_t w[2] = {vc[k].x & keep, vc[k].y & keep};
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], false);  // bytes 0, 1
+                    const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], true);   // bytes 2, 3
+                    v[4 * q] = f0[0]; v[4 * q + 1] = f0[1]; v[4 * q + 2] = f1[0]; v[4 * q + 3] = f1[1];
+                }
+            }
             float p[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) p[h] = p_lds[4 * k + grp][h];
