@@ -13,9 +13,14 @@
  *   - zero-sized work returns 0 without launching (device/cpu/layernorm/compute.go:19-21);
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
  *     Launches are asynchronous: no entry point synchronises the host, matching
- *     the zero-host-sync rule the reference's interface documents;
- *   - the library never allocates on an op path; the caller owns every buffer
- *     (workspaces included, see puter_hip_paged_decode_workspace_bytes).
+ *     the zero-host-sync rule the reference's interface documents (one
+ *     exception, below);
+ *   - the caller owns every buffer (workspaces included, see
+ *     puter_hip_paged_decode_workspace_bytes).  The one allocation the library
+ *     makes itself is puter_hip_matmul's split-K scratch (16-bit formats, at
+ *     most 512 rows): one device buffer per device, allocated on first use and
+ *     grown on demand (at most ~16 MB); a growth waits on the host for the
+ *     buffer's last user before freeing it.
  *
  * Status codes follow the reference's CUDA bridge (device/cuda/internal/bridge/status.c):
  *   -2 nil buffer, -6 invalid dtype / shape / config, -7 device unavailable,
@@ -331,6 +336,12 @@ PUTER_API int puter_hip_quant(void *dst, const void *src, int64_t count, float s
 /* ------------------------------------------------------------------------ */
 /* Matmul: device/interface.go:409-415 (F32), device/cpu/matmul/compute.go:46-62 */
 /* ------------------------------------------------------------------------ */
+/* out[rows, cols] = left[rows, inner] . right[inner, cols], row-major, in F32, F64,
+ * BF16 or F16 (16-bit formats accumulate in f32 and round once).  BF16 / F16 with
+ * cols % 8 == 0, inner % 8 == 0 and 16-byte aligned buffers run on MFMA; with at
+ * most 512 rows they split `inner` across blocks and keep f32 partials in the
+ * library's per-device scratch (calls on different streams are ordered on the
+ * device by an event).  inner == 0 writes zeros. */
 PUTER_API int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,
                      int64_t inner, int64_t cols, int dtype, void *stream);
 
