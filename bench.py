@@ -302,6 +302,34 @@ def matmul_bf16(torch, be, puter):
     return res
 
 
+def block_bf16(torch, be, puter):
+    """configs[0]'s block in bf16 storage (the same chain and shapes as block_f32,
+    each op rounding its output to bf16): GPU latency per block."""
+    S, HID, H, D = 128, 512, 8, 64
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0007)
+    bf = torch.bfloat16
+    x = torch.randn(S * HID, device="cuda", generator=gen).to(bf)
+    g = (1 + 0.02 * torch.randn(HID, device="cuda", generator=gen)).to(bf)
+    W = [(0.02 * torch.randn(HID * HID, device="cuda", generator=gen)).to(bf) for _ in range(4)]
+    h, q, k, v, o, y = (torch.empty(S * HID, device="cuda", dtype=bf) for _ in range(6))
+    ncfg = puter.RMSNormConfig(1e-6)
+    rcfg = puter.RoPEConfig(BaseFreq=10000.0)
+    mcfg = puter.MultiHeadAttentionConfig(H, D, True, 0, 0.0, H)
+
+    def chain():
+        be.RMSNorm(ncfg, x, g, h, S, HID, puter.BF16)
+        be.Matmul(q, h, W[0], S, HID, HID, puter.BF16)
+        be.Matmul(k, h, W[1], S, HID, HID, puter.BF16)
+        be.Matmul(v, h, W[2], S, HID, HID, puter.BF16)
+        be.RoPE(rcfg, q, q, S, H, D, puter.BF16)
+        be.RoPE(rcfg, k, k, S, H, D, puter.BF16)
+        be.MultiHeadAttention(mcfg, q, k, v, o, S, S, puter.BF16)
+        be.Matmul(y, o, W[3], S, HID, HID, puter.BF16)
+
+    t = Timer(torch).time(chain, 50, warmup=3)
+    return {"block_bf16_us": round(t * 1e3, 1)}
+
+
 def block_f32(torch, be, puter):
     """one pre-norm attention block in f32, batch 1, seq 128, hidden
     512, 8 heads x 64: RMSNorm (eps 1e-6, gamma 1+N(0,.02)) -> Q/K/V projections
@@ -592,6 +620,7 @@ def main():
         log(f"matmul bf16: {configs['matmul_bf16_8192c_TFLOPs']} TFLOP/s at 8192^3")
     if "block" in only:
         configs.update(block_f32(torch, be, puter))
+        configs.update(block_bf16(torch, be, puter))
         log(f"block f32: {configs['block_f32_us']} us, err {configs['block_f32_normwise_err']:.2e}")
     cpu = cpu_baseline() if "cpu" in only else None
     if "cpu" in only:
