@@ -17,8 +17,8 @@
  *     exception, below);
  *   - the caller owns every buffer (workspaces included, see
  *     puter_hip_paged_decode_workspace_bytes).  The one allocation the library
- *     makes itself is puter_hip_matmul's split-K scratch (16-bit formats, at
- *     most 512 rows): one device buffer per device, allocated on first use and
+ *     makes itself is puter_hip_matmul's split-K scratch (16-bit formats with
+ *     at most 512 rows, F32 outputs of fewer than 256 64x64 tiles): one buffer per device, allocated on first use and
  *     grown on demand (at most ~16 MB); a growth waits on the host for the
  *     buffer's last user before freeing it.
  *
@@ -341,7 +341,8 @@ PUTER_API int puter_hip_quant(void *dst, const void *src, int64_t count, float s
  * cols % 8 == 0, inner % 8 == 0 and 16-byte aligned buffers run on MFMA; with at
  * most 512 rows they split `inner` across blocks and keep f32 partials in the
  * library's per-device scratch (calls on different streams are ordered on the
- * device by an event).  inner == 0 writes zeros. */
+ * device by an event); so does F32 when the output has fewer than 256 64x64
+ * tiles.  inner == 0 writes zeros. */
 PUTER_API int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,
                      int64_t inner, int64_t cols, int dtype, void *stream);
 

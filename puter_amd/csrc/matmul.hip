@@ -36,7 +36,8 @@
 // kernel (one thread per output, f32 accumulation in index order).
 //
 // f32: 64 x 64 output tile per 256-thread block, 16-deep K slices in LDS, 4 x 4
-// register micro-tile, f32 FMA.  f64: one thread per output, f64 sum in index
+// register micro-tile, f32 FMA; grids of fewer than 256 tiles split K across
+// blocks (f32 partials summed in chunk order).  f64: one thread per output, f64 sum in index
 // order (matmulFloat64Scalar, device/cpu/matmul/select_generic.go:39-...).
 #include "common.hpp"
 #include <algorithm>
@@ -48,16 +49,21 @@ namespace puter {
 // ------------------------------------------------------------------- f32 --
 constexpr int kTile = 64, kDepth = 16;
 
+// Block (x, y, z) computes output tile (y, x) over K range [z kc, (z + 1) kc) (kc a
+// multiple of kDepth); with ws set it stores its partial tile to ws[z] instead of
+// the result (split K for grids too small to fill the GPU).
 __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out,
                                                          const float *__restrict__ A,
                                                          const float *__restrict__ B,
-                                                         int64_t M, int64_t K, int64_t N) {
+                                                         int64_t M, int64_t K, int64_t N,
+                                                         float *__restrict__ ws, int64_t kc) {
     __shared__ float As[kDepth][kTile + 4];
     __shared__ float Bs[kDepth][kTile + 4];
     const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
     const int64_t row0 = (int64_t)blockIdx.y * kTile, col0 = (int64_t)blockIdx.x * kTile;
+    const int64_t kbeg = (int64_t)blockIdx.z * kc, kend = std::min(K, kbeg + kc);
     float acc[4][4] = {};
-    for (int64_t k0 = 0; k0 < K; k0 += kDepth) {
+    for (int64_t k0 = kbeg; k0 < kend; k0 += kDepth) {
         for (int i = threadIdx.x; i < kTile * kDepth; i += 256) {
             const int r = i / kDepth, c = i % kDepth;          // A tile: 64 rows x 16
             const int64_t gr = row0 + r, gc = k0 + c;
@@ -86,7 +92,10 @@ __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t r = row0 + ty * 4 + i, c = col0 + tx * 4 + j;
-            if (r < M && c < N) out[r * N + c] = acc[i][j];
+            if (r < M && c < N) {
+                if (ws) ws[((int64_t)blockIdx.z * M + r) * N + c] = acc[i][j];
+                else out[r * N + c] = acc[i][j];
+            }
         }
 }
 
@@ -622,6 +631,47 @@ static int launch_matmul16(void *out, const void *left, const void *right, int64
 
 using namespace puter;
 
+// out = sum over chunks z = 0, 1, ... of ws[z] (f32)
+__global__ __launch_bounds__(256) void matmul_splitk_reduce_f32_kernel(float *c, const float *ws, int64_t n,
+                                                                       int chunks) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        float t = ws[i];
+        for (int z = 1; z < chunks; ++z) t += ws[(int64_t)z * n + i];
+        c[i] = t;
+    }
+}
+
+// f32: 64 x 64 tiles; grids of fewer than 256 tiles split K (16-deep steps) into as
+// many chunks as keep the grid within 512 blocks, partials in the split-K scratch.
+static int launch_matmul_f32(float *out, const float *left, const float *right, int64_t M, int64_t K, int64_t N,
+                             hipStream_t s) {
+    const dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
+    if (grid.y > 65535) return fail(PUTER_ERR_INVALID, "matmul: too many rows");
+    const int64_t tiles = (int64_t)grid.x * grid.y, steps = (K + kDepth - 1) / kDepth;
+    int64_t chunks = tiles < 256 ? std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(512 / tiles, 1), steps), 64) : 1;
+    const int64_t per = (steps + chunks - 1) / chunks;
+    chunks = (steps + per - 1) / per;
+    if (chunks == 1) {
+        matmul_f32_kernel<<<grid, 256, 0, s>>>(out, left, right, M, K, N, nullptr, K);
+        return check_launch("matmul");
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(PUTER_ERR_UNAVAILABLE, "matmul: no device");
+    SplitScratch &sc = g_split_scratch[dev];
+    std::lock_guard<std::mutex> lock(sc.mu);
+    if (int rc = scratch_acquire(sc, (size_t)(chunks * M * N) * sizeof(float), s)) return rc;
+    float *ws = static_cast<float *>(sc.ptr);
+    matmul_f32_kernel<<<dim3(grid.x, grid.y, (unsigned)chunks), 256, 0, s>>>(out, left, right, M, K, N, ws,
+                                                                               per * kDepth);
+    matmul_splitk_reduce_f32_kernel<<<(unsigned)std::min<int64_t>((M * N + 255) / 256, 4096), 256, 0, s>>>(
+        out, ws, M * N, (int)chunks);
+    const int rc = check_launch("matmul split-k");
+    if (hipEventRecord(sc.done, s) != hipSuccess) return fail(PUTER_ERR_LAUNCH, "matmul: cannot record the split-K event");
+    sc.last = s;
+    sc.used = true;
+    return rc;
+}
+
 extern "C" int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,
                                 int64_t inner, int64_t cols, int dtype, void *stream) {
     if (rows < 0 || inner < 0 || cols < 0) return fail(PUTER_ERR_INVALID, "matmul: negative shape");
@@ -644,9 +694,6 @@ extern "C" int puter_hip_matmul(void *out, const void *left, const void *right, 
         return check_launch("matmul");
     default: break;
     }
-    const dim3 grid((unsigned)((cols + kTile - 1) / kTile), (unsigned)((rows + kTile - 1) / kTile));
-    if (grid.y > 65535) return fail(PUTER_ERR_INVALID, "matmul: too many rows");
-    matmul_f32_kernel<<<grid, 256, 0, s>>>(static_cast<float *>(out), static_cast<const float *>(left),
-                                           static_cast<const float *>(right), rows, inner, cols);
-    return check_launch("matmul");
+    return launch_matmul_f32(static_cast<float *>(out), static_cast<const float *>(left),
+                             static_cast<const float *>(right), rows, inner, cols, s);
 }

@@ -171,6 +171,25 @@ def test_matmul_f64_and_f32(backend):
         assert np.allclose(to_host(out, np.float64), ref, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("rows,inner,cols", [(128, 512, 512), (100, 1000, 300), (64, 96, 48), (7, 13, 5),
+                                             (300, 40, 1100)])
+def test_matmul_f32_split_k(backend, rows, inner, cols):
+    """F32 (config 1's Matmul): grids of fewer than 256 64x64 tiles split K into
+    16-deep-step chunks summed in order; ragged shapes and a K tail, against the
+    oracle's index-order f32 sum at the f32 bar, and two calls bit-identical."""
+    a = seeded(rows * 5 + inner, (rows, inner))
+    b = seeded(cols * 3 + inner, (inner, cols), 0.0, 0.05)
+    ref = O.matmul_f32(a, b)
+    ad, bd = to_dev(a), to_dev(b)
+    out = empty_dev((rows, cols), np.float32)
+    backend.Matmul(out, ad, bd, rows, inner, cols, O.F32)
+    got = to_host(out, np.float32)
+    assert_close(got, ref, TOL[O.F32], elem_tol=1e-3, what="f32 matmul %dx%dx%d" % (rows, inner, cols))
+    out2 = empty_dev((rows, cols), np.float32)
+    backend.Matmul(out2, ad, bd, rows, inner, cols, O.F32)
+    assert np.array_equal(to_host(out2, np.float32), got)
+
+
 @pytest.mark.parametrize("dt,np_dt", [(O.BF16, np.uint16), (O.F32, np.float32), (O.F64, np.float64)])
 def test_matmul_empty_inner_is_zero(backend, dt, np_dt):
     rows, cols = 5, 7   # odd element count
