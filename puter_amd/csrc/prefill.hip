@@ -1,5 +1,5 @@
-// MFMA flash-attention prefill: bf16 Q/K/V, f32 accumulation, bf16 output,
-// head_dim 128, GQA, optional causal mask: key k is visible to query q when
+// MFMA flash-attention prefill: bf16 or f16 Q/K/V (prefill_d128_kernel<dtype>),
+// f32 accumulation, output in the input format, head_dim 128, GQA, optional causal mask: key k is visible to query q when
 // k <= q + shift.  MultiHeadAttention passes shift = seqK - seqQ (bottom-right
 // aligned, device/cpu/attention/typed_compute.go:166-168);
 // ScaledDotProductAttention passes 0 (typed_compute.go:60-62).
@@ -57,6 +57,21 @@ namespace puter {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// element, fragment types and MFMA of the two 16-bit formats
+template <int DT> struct PfFormat;
+template <> struct PfFormat<PUTER_BF16> {
+    using E = __bf16;
+    using V8 = bf16x8;
+    using V4 = bf16x4;
+};
+template <> struct PfFormat<PUTER_F16> {
+    using E = _Float16;
+    using V8 = f16x8;
+    using V4 = f16x4;
+};
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -130,10 +145,19 @@ __device__ __forceinline__ void prefill_copy_tile(const PrefillArgs &a, const ui
 // sequence-end mask (diagonal and tail tiles only).  ka / va: this lane's byte
 // offsets of its K fragments (per 16-dim step t) and V^T fragments (per
 // 32-dim block d) inside a tile.
+template <int DT>
+__device__ __forceinline__ f32x16 pf_mfma(typename PfFormat<DT>::V8 a, typename PfFormat<DT>::V8 b, f32x16 c) {
+    if constexpr (DT == PUTER_BF16) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int DT>
 __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *ks, const char *vs,
-                                             const bf16x8 (&qf)[8], PrefillState &st, int qi, int kv0,
-                                             const int (&ka)[8], const int (&va)[4], int g, bool masked) {
+                                             const typename PfFormat<DT>::V8 (&qf)[8], PrefillState &st, int qi,
+                                             int kv0, const int (&ka)[8], const int (&va)[4], int g, bool masked) {
     using namespace fa;
+    using V8 = typename PfFormat<DT>::V8;
+    using E = typename PfFormat<DT>::E;
     // S^T chunks: keys kv0 + 32c + (8*(r/4) + 4g + r%4), query qi; two
     // independent accumulation chains interleaved
     f32x16 s[2] = {(f32x16){}, (f32x16){}};
@@ -141,9 +165,17 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
     for (int t = 0; t < 8; ++t)
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(ks + c * 8192 + ka[t]);
-            s[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], s[c], 0, 0, 0);
+            const V8 kf = *reinterpret_cast<const V8 *>(ks + c * 8192 + ka[t]);
+            s[c] = pf_mfma<DT>(kf, qf[t], s[c]);
         }
+    if constexpr (DT == PUTER_F16) {
+        // f16 dots are rounded to f16 as the reference's typed row dot does
+        // (attention/typed_compute.go:16-20); bf16 keeps the f32 dot
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[c][r] = (float)(_Float16)s[c][r];
+    }
     if (masked) {
         // key kv0 + 32c + 8(r/4) + 4g + r%4 is visible iff its offset past
         // kv0 + 4g is <= lim (the query's last visible key, relative)
@@ -160,7 +192,7 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
     // bounds every p as the max test would.  Otherwise (first tile, or a score
     // far above the reference) the max is taken, O and l rescaled, p redone.
     float psum = 0.0f;
-    bf16x8 pf[2][2];
+    V8 pf[2][2];
     bool done = false;
     if (!__any(st.m == -INFINITY)) {
 #pragma unroll
@@ -171,7 +203,7 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
                 for (int j = 0; j < 8; ++j) {
                     const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][8 * h + j], a.scale_log2, -st.m));
                     psum += p;
-                    pf[c][h][j] = (__bf16)p;
+                    pf[c][h][j] = (E)p;
                 }
         done = !__any(psum > RESCALE_LIMIT);  // each p of this lane <= its partial sum
     }
@@ -202,7 +234,7 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
                 for (int j = 0; j < 8; ++j) {
                     const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][8 * h + j], a.scale_log2, -mref));
                     psum += p;
-                    pf[c][h][j] = (__bf16)p;
+                    pf[c][h][j] = (E)p;
                 }
     }
     st.l += psum;
@@ -217,13 +249,17 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
                 const char *p = vs + (32 * c + 16 * h) * 256 + va[d];
                 const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
                 const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * 256));
-                const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                st.o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[c][h], st.o[d], 0, 0, 0);
+                const V8 vf = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                st.o[d] = pf_mfma<DT>(vf, pf[c][h], st.o[d]);
             }
 }
 
-__global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a) {
+template <int DT>
+__global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
     using namespace fa;
+    using V8 = typename PfFormat<DT>::V8;
+    using V4 = typename PfFormat<DT>::V4;
+    using E = typename PfFormat<DT>::E;
     // four separate arrays (not one indexed by parity) so the compiler can
     // tell the tile being copied from the tile being read and does not wait
     // for the copy before the reads
@@ -268,12 +304,12 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
     const int qfirst = q0 + 32 * wave;
     const int qlast = min(qfirst + 31, a.seq_q - 1);
     const int qi = qfirst + l32;
-    bf16x8 qf[8];
+    V8 qf[8];
     {
         const int qload = min(qi, a.seq_q - 1);  // rows past the end compute garbage, never stored
 #pragma unroll
         for (int t = 0; t < 8; ++t)
-            qf[t] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(qbase + (int64_t)qload * qrs + 16 * t + 8 * g));
+            qf[t] = __builtin_bit_cast(V8, *reinterpret_cast<const uint4 *>(qbase + (int64_t)qload * qrs + 16 * t + 8 * g));
     }
 
     // key tiles of the block: [0, ntiles); tiles [0, nfree) need no mask for any query of it
@@ -327,7 +363,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
         if (it + 1 < ntiles) prefill_copy_tile(a, kbase, vbase, kv0 + BN, kg, vg, kn, vn, wave);
         // waves whose queries all precede this tile skip it
         if (!a.causal || kv0 <= qlast + a.shift)
-            prefill_step(a, kc, vc, qf, st, qi, kv0, ka, va, g, it >= nfree);
+            prefill_step<DT>(a, kc, vc, qf, st, qi, kv0, ka, va, g, it >= nfree);
         wait_tile_copies();
         __syncthreads();
     };
@@ -347,16 +383,16 @@ __global__ __launch_bounds__(256, 2) void prefill_bf16_d128_kernel(PrefillArgs a
         for (int d = 0; d < 4; ++d)
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
-                bf16x4 v;
+                V4 v;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = (__bf16)(st.o[d][4 * rb + i] * inv);
-                *reinterpret_cast<bf16x4 *>(orow + 32 * d + 8 * rb + 4 * g) = v;
+                for (int i = 0; i < 4; ++i) v[i] = (E)(st.o[d][4 * rb + i] * inv);
+                *reinterpret_cast<V4 *>(orow + 32 * d + 8 * rb + 4 * g) = v;
             }
     }
 }
 
 bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
-    if (dtype != PUTER_BF16 || m.dim != 128 || m.window > 0 || m.alibi != 0.0f) return false;
+    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || m.dim != 128 || m.window > 0 || m.alibi != 0.0f) return false;
     if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF)
         return false;
     // 32-bit buffer offsets: one 64-row tile of K/V must span < 2^31 bytes
@@ -382,7 +418,8 @@ bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status
     a.scale_log2 = m.scale * 1.4426950408889634f;
     const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;
     if (blocks > 0x7FFFFFFF) return false;
-    prefill_bf16_d128_kernel<<<(unsigned)blocks, 256, 0, s>>>(a);
+    if (dtype == PUTER_BF16) prefill_d128_kernel<PUTER_BF16><<<(unsigned)blocks, 256, 0, s>>>(a);
+    else prefill_d128_kernel<PUTER_F16><<<(unsigned)blocks, 256, 0, s>>>(a);
     *status = check_launch("prefill mfma");
     return true;
 }

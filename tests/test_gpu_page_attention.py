@@ -134,7 +134,7 @@ def test_page_out_of_range_ids_never_touch_memory(backend):
 
 
 # -------------------------------------------------------------- attention --
-@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16])
 @pytest.mark.parametrize("sq,sk,h,kvh,d,causal", [
     (128, 128, 8, 8, 64, True),     # config 1
     (77, 77, 4, 2, 64, True),
@@ -190,9 +190,10 @@ def test_mha_batched_prefill_bf16(backend):
     (1, 130, 77, 8, 8, False),      # non-causal, seqK < 64-key tile
     (1, 96, 40, 4, 2, True),        # seqQ > seqK: leading queries see no key -> zeros
 ])
-def test_prefill_mfma_shapes(backend, b, sq, sk, h, kvh, causal):
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+def test_prefill_mfma_shapes(backend, dt, b, sq, sk, h, kvh, causal):
     import puter_amd
-    dt, d = O.BF16, 128
+    d = 128
     std = 1.0 / np.sqrt(d)
     q = encode(seeded(300 + sq, (b, sq, h * d), 0.0, std), dt)
     k = encode(seeded(301 + sk, (b, sk, kvh * d), 0.0, std), dt)
