@@ -107,7 +107,7 @@ static int run_flash(const puter_flash_config *config, const void *q, const void
     if (seq_q > 0x7FFFFFFF) return fail(PUTER_ERR_INVALID, "flash attention: grid too large");
     if (!q || !k || !v || !o) return fail(PUTER_ERR_NIL, "flash attention: nil buffer");
     const float scale = (float)(1.0 / sqrt((double)depth));
-    if (dtype == PUTER_BF16 && depth == 128 && value_dim == 128) {
+    if ((dtype == PUTER_BF16 || dtype == PUTER_F16) && depth == 128 && value_dim == 128) {
         MhaArgs m{q, k, v, o, 1, seq_q, seq_k, 1, 1, 128, config->causal ? 1 : 0, 0, 0.0f, scale, 0};
         int status = PUTER_OK;
         if (launch_prefill_mfma(m, dtype, s, &status)) return status;

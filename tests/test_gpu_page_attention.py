@@ -215,8 +215,8 @@ def test_prefill_mfma_shapes(backend, dt, b, sq, sk, h, kvh, causal):
     (37, 37, 64, 64, True),
     (20, 300, 48, 24, True),        # top-left causal with seqK > seqQ
     (300, 20, 32, 80, True),        # later rows see every key
-    (65, 513, 128, 128, False),     # bf16 here takes the MFMA kernel
-    (200, 700, 128, 128, True),     # bf16 MFMA path, top-left causal
+    (65, 513, 128, 128, False),     # bf16 / f16 here take the MFMA kernel
+    (200, 700, 128, 128, True),     # bf16 / f16 MFMA path, top-left causal
     (3, 5, 1000, 1000, False),      # wide rows, four output dims per thread
 ])
 def test_scaled_dot_product_attention(backend, dt, sq, sk, d, vd, causal):
