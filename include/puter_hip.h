@@ -17,8 +17,10 @@
  *     exception, below);
  *   - the caller owns every buffer (workspaces included, see
  *     puter_hip_paged_decode_workspace_bytes).  The one allocation the library
- *     makes itself is puter_hip_matmul's split-K scratch (16-bit formats with
- *     at most 512 rows, F32 outputs of fewer than 256 64x64 tiles): one buffer per device, allocated on first use and
+ *     makes itself is a split-K scratch shared by puter_hip_matmul (16-bit
+ *     formats with at most 512 rows, F32 outputs of fewer than 256 64x64 tiles)
+ *     and puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16, head
+ *     dim 128): one buffer per device, allocated on first use and
  *     grown on demand (at most ~16 MB); a growth waits on the host for the
  *     buffer's last user before freeing it.
  *

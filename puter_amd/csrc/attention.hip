@@ -94,6 +94,7 @@ static int run_mha(const puter_mha_config *config, const void *q, const void *k,
     MhaArgs a{q, k, v, o, batch, seq_q, seq_k, H, kvh, D, config->causal ? 1 : 0,
               config->window_size, config->alibi_slope, (float)(1.0 / sqrt((double)D)), seq_k - seq_q};
     int status = PUTER_OK;
+    if (launch_decode_contiguous(a, dtype, s, &status)) return status;
     if (launch_prefill_mfma(a, dtype, s, &status)) return status;
     const dim3 grid((unsigned)seq_q, (unsigned)H, (unsigned)batch);
     switch (dtype) {

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <cstdio>
 #include <string>
 
@@ -17,6 +18,28 @@ void set_error(const char *fmt, ...);
 int fail(int status, const char *fmt, ...);
 int check_launch(const char *what);
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// The library's scratch buffer on the current device (split-K partials of Matmul
+// and of one-row attention), held for one call's launches: the constructor orders
+// the call's stream after the buffer's last user on another stream and grows the
+// buffer if needed; finish() records the call's completion on its stream.  The
+// device's lock is held from construction to destruction.
+struct SplitScratch;
+class ScratchLease {
+public:
+    ScratchLease(size_t bytes, hipStream_t s);
+    ScratchLease(const ScratchLease &) = delete;
+    ScratchLease &operator=(const ScratchLease &) = delete;
+    int status() const { return status_; }
+    void *ptr() const { return ptr_; }
+    int finish();  // call once, after the launches that use ptr()
+private:
+    SplitScratch *sc_ = nullptr;
+    std::unique_lock<std::mutex> lock_;
+    hipStream_t s_;
+    void *ptr_ = nullptr;
+    int status_ = 0;
+};
 
 inline bool is_float_dtype(int dt) { return dt >= PUTER_F32 && dt <= PUTER_F8E5M2; }
 inline bool is_norm_dtype(int dt) { return dt == PUTER_F32 || dt == PUTER_F16 || dt == PUTER_BF16; }

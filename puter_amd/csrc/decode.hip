@@ -27,6 +27,7 @@
 // The 4 token-group partials are summed in registers (lane-row swaps) into one
 // (m, l, o[D]) per query head and split; decode_combine_kernel merges the
 // splits by log-sum-exp.
+#include "attention.hpp"
 #include "common.hpp"
 #include <algorithm>
 #include <type_traits>
@@ -78,9 +79,9 @@ __device__ __forceinline__ uint4 fp8x8_to_bf16(uint2 raw) {
 // (bf16) or 8-byte (fp8) piece l16.  K rows then pass through a wave-private
 // LDS tile (piece p of row r stored at p ^ swizzle(r)) to reach the MFMA
 // operand layout, 16 rows x one piece per read, bank-conflict free.
-template <int KV, int G>
+template <int KV, int G, int SPLIT = kSplit>
 __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a) {
-    constexpr int D = 128, SUB = 32, NSUB = kSplit / SUB, NGRP = kSplit / 64;
+    constexpr int D = 128, SUB = 32, NSUB = SPLIT / SUB, NGRP = (SPLIT + 63) / 64;
     constexpr bool BF = KV == PUTER_BF16;
     constexpr int RB = BF ? 256 : 128;            // KV row bytes
     using VT = typename std::conditional<BF, uint4, uint2>::type;
@@ -88,14 +89,16 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
     __shared__ float p_lds[SUB][G];               // probabilities [token][head]
 
     const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
-    const int ctx = (int)min((int64_t)a.ctx[b], a.max_context);
-    const int t0 = split * kSplit;
+    // (null ctx / table: every sequence holds max_context tokens in contiguous rows,
+    // sequence b's token t at row b * page_size + t - one-row MultiHeadAttention)
+    const int ctx = a.ctx ? (int)min((int64_t)a.ctx[b], a.max_context) : (int)a.max_context;
+    const int t0 = split * SPLIT;
     if (t0 >= ctx) return;
     const int lane = threadIdx.x, l16 = lane & 15, grp = lane >> 4;
     const int nsub = min(NSUB, (ctx - t0 + SUB - 1) / SUB);
     const int64_t inner = a.kv_heads * D;
     const int ps = (int)a.page_size;
-    const int32_t *table = a.table + (int64_t)b * a.max_pages;
+    const int32_t *table = a.table ? a.table + (int64_t)b * a.max_pages : nullptr;
     const int64_t head_off = (int64_t)kvh * D;
     const uint8_t *kpool = static_cast<const uint8_t *>(a.kp);
     const uint8_t *vpool = static_cast<const uint8_t *>(a.vp);
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
         const int tok = t0 + 64 * n + lane;
         if (tok < ctx) {
             const int pidx = tok / ps;
-            const int32_t page = table[pidx];
+            const int32_t page = table ? table[pidx] : b * (int)a.max_pages + pidx;
             if (page >= 0 && page < a.num_pages) myrow[n] = page * ps + (tok - pidx * ps);
         }
     }
@@ -292,12 +295,12 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 // sequence's split partials by log-sum-exp.  The (m, l) pairs are read by
 // all threads (the same addresses: one transaction), the split loop is
 // unrolled 4-wide so its loads are in flight together.
-template <int KV>
+template <int KV, int SPLIT = kSplit>
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
     constexpr int D = 128;
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const int ctx = (int)min((int64_t)a.ctx[b], a.max_context);
-    const int nsplit = (ctx + kSplit - 1) / kSplit;
+    const int ctx = a.ctx ? (int)min((int64_t)a.ctx[b], a.max_context) : (int)a.max_context;
+    const int nsplit = (ctx + SPLIT - 1) / SPLIT;
     const int64_t base = ((int64_t)b * a.heads + h) * a.max_splits;
     const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + base;
     const float *po = a.part_o + base * D + d;
@@ -342,6 +345,66 @@ static int64_t splits_for(int64_t max_context) { return (max_context + kSplit - 
 }  // namespace puter
 
 using namespace puter;
+
+namespace puter {
+
+// MultiHeadAttention with one query row per sequence (the reference's decode step:
+// gathered K/V, seqQ 1, typed_compute.go:206-237), bf16, head_dim 128, no window or
+// ALiBi: the paged decode kernels over the contiguous K/V (sequence b's keys are
+// page b of seq_k rows), partials in the library's scratch.  A causal mask with
+// one query row sees every key (bottom-right alignment), as does no mask.
+bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
+    if (dtype != PUTER_BF16 || m.dim != 128 || m.seq_q != 1 || m.window > 0 || m.alibi != 0.0f) return false;
+    const int64_t G = m.heads / m.kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return false;
+    if (!aligned16(m.q) || !aligned16(m.k) || !aligned16(m.v) || !aligned16(m.o)) return false;
+    if (m.batch > 65535 || m.seq_k > 0x7FFFFFFF / std::max<int64_t>(m.batch, 1) || m.kv_heads > 0x7FFFFFFF)
+        return false;
+    // 64-token splits (2 sub-chunks per wave) while 256-token splits would give fewer
+    // than 256 waves: a wave's sub-chunks run one after another, so few long splits
+    // are latency-bound (one sequence, 32 heads over 8: 4096 keys 24 -> 20 us; at
+    // 8192 keys the 256-token splits are already faster, 26 vs 29 us)
+    const bool short_splits = m.batch * m.kv_heads * splits_for(m.seq_k) < 256;
+    const int split = short_splits ? 64 : kSplit;
+    const int64_t splits = (m.seq_k + split - 1) / split;
+    if (splits > 65535) return false;
+    const size_t need = (size_t)(m.batch * m.heads * splits) * (128 + 2) * sizeof(float);
+    ScratchLease lease(need, s);
+    if (lease.status()) {
+        *status = lease.status();
+        return true;
+    }
+    float *ws = static_cast<float *>(lease.ptr());
+    const int64_t slots = m.batch * m.heads * splits;
+    DecodeArgs a{static_cast<const uint16_t *>(m.q), m.k, m.v, nullptr, nullptr, nullptr, nullptr,
+                 static_cast<uint16_t *>(m.o), ws, ws + slots * 128, m.batch, 1, m.seq_k, m.batch, m.heads,
+                 m.kv_heads, splits, m.seq_k, m.scale};
+    const dim3 grid((unsigned)m.kv_heads, (unsigned)splits, (unsigned)m.batch);
+    const dim3 cgrid((unsigned)m.heads, (unsigned)m.batch);
+    if (short_splits) {
+        switch (G) {
+        case 1: decode_kernel<PUTER_BF16, 1, 64><<<grid, 64, 0, s>>>(a); break;
+        case 2: decode_kernel<PUTER_BF16, 2, 64><<<grid, 64, 0, s>>>(a); break;
+        case 4: decode_kernel<PUTER_BF16, 4, 64><<<grid, 64, 0, s>>>(a); break;
+        case 8: decode_kernel<PUTER_BF16, 8, 64><<<grid, 64, 0, s>>>(a); break;
+        }
+        decode_combine_kernel<PUTER_BF16, 64><<<cgrid, 128, 0, s>>>(a);
+    } else {
+        switch (G) {
+        case 1: decode_kernel<PUTER_BF16, 1><<<grid, 64, 0, s>>>(a); break;
+        case 2: decode_kernel<PUTER_BF16, 2><<<grid, 64, 0, s>>>(a); break;
+        case 4: decode_kernel<PUTER_BF16, 4><<<grid, 64, 0, s>>>(a); break;
+        case 8: decode_kernel<PUTER_BF16, 8><<<grid, 64, 0, s>>>(a); break;
+        }
+        decode_combine_kernel<PUTER_BF16><<<cgrid, 128, 0, s>>>(a);
+    }
+    const int rc = check_launch("mha one-row decode");
+    const int fin = lease.finish();
+    *status = rc ? rc : fin;
+    return true;
+}
+
+}  // namespace puter
 
 extern "C" {
 

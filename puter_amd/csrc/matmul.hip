@@ -569,6 +569,26 @@ static int scratch_acquire(SplitScratch &sc, size_t need, hipStream_t s) {
     return PUTER_OK;
 }
 
+ScratchLease::ScratchLease(size_t bytes, hipStream_t s) : s_(s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        status_ = fail(PUTER_ERR_UNAVAILABLE, "scratch: no device");
+        return;
+    }
+    sc_ = &g_split_scratch[dev];
+    lock_ = std::unique_lock<std::mutex>(sc_->mu);
+    status_ = scratch_acquire(*sc_, bytes, s);
+    if (status_ == PUTER_OK) ptr_ = sc_->ptr;
+}
+
+int ScratchLease::finish() {
+    if (status_ != PUTER_OK) return status_;
+    if (hipEventRecord(sc_->done, s_) != hipSuccess) return fail(PUTER_ERR_LAUNCH, "scratch: cannot record the event");
+    sc_->last = s_;
+    sc_->used = true;
+    return PUTER_OK;
+}
+
 // Returns 1 when the shape does not fit the skinny kernel.
 template <int DT>
 static int launch_skinny(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
@@ -590,21 +610,16 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
         matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
         return check_launch("matmul skinny");
     }
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(PUTER_ERR_UNAVAILABLE, "matmul: no device");
-    SplitScratch &sc = g_split_scratch[dev];
-    std::lock_guard<std::mutex> lock(sc.mu);
-    if (int rc = scratch_acquire(sc, (size_t)(chunks * M * N) * sizeof(float), s)) return rc;
-    p.ws = static_cast<float *>(sc.ptr);
+    ScratchLease lease((size_t)(chunks * M * N) * sizeof(float), s);
+    if (lease.status()) return lease.status();
+    p.ws = static_cast<float *>(lease.ptr());
     matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
     const int64_t quads = M * N / 4;
     matmul_splitk_reduce_kernel<DT><<<(unsigned)std::min<int64_t>((quads + 255) / 256, 4096), 256, 0, s>>>(
         static_cast<uint16_t *>(out), p.ws, quads, (int)chunks);
     const int rc = check_launch("matmul split-k");
-    if (hipEventRecord(sc.done, s) != hipSuccess) return fail(PUTER_ERR_LAUNCH, "matmul: cannot record the split-K event");
-    sc.last = s;
-    sc.used = true;
-    return rc;
+    const int fin = lease.finish();
+    return rc ? rc : fin;
 }
 
 template <int DT>
@@ -655,21 +670,16 @@ static int launch_matmul_f32(float *out, const float *left, const float *right, 
         matmul_f32_kernel<<<grid, 256, 0, s>>>(out, left, right, M, K, N, nullptr, K);
         return check_launch("matmul");
     }
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(PUTER_ERR_UNAVAILABLE, "matmul: no device");
-    SplitScratch &sc = g_split_scratch[dev];
-    std::lock_guard<std::mutex> lock(sc.mu);
-    if (int rc = scratch_acquire(sc, (size_t)(chunks * M * N) * sizeof(float), s)) return rc;
-    float *ws = static_cast<float *>(sc.ptr);
+    ScratchLease lease((size_t)(chunks * M * N) * sizeof(float), s);
+    if (lease.status()) return lease.status();
+    float *ws = static_cast<float *>(lease.ptr());
     matmul_f32_kernel<<<dim3(grid.x, grid.y, (unsigned)chunks), 256, 0, s>>>(out, left, right, M, K, N, ws,
                                                                                per * kDepth);
     matmul_splitk_reduce_f32_kernel<<<(unsigned)std::min<int64_t>((M * N + 255) / 256, 4096), 256, 0, s>>>(
         out, ws, M * N, (int)chunks);
     const int rc = check_launch("matmul split-k");
-    if (hipEventRecord(sc.done, s) != hipSuccess) return fail(PUTER_ERR_LAUNCH, "matmul: cannot record the split-K event");
-    sc.last = s;
-    sc.used = true;
-    return rc;
+    const int fin = lease.finish();
+    return rc ? rc : fin;
 }
 
 extern "C" int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,

@@ -156,6 +156,33 @@ def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
                  elem_tol=1e-3 if dt == O.F32 else None, what="mha")
 
 
+@pytest.mark.parametrize("b,sk,h,kvh,causal", [
+    (1, 4096, 32, 8, True),     # configs[4]'s heads at one sequence's full context
+    (1, 100, 8, 8, False),      # group size 1, part of one split
+    (1, 300, 16, 2, True),      # group size 8
+    (3, 700, 8, 4, True),       # batched, partial last split
+])
+def test_mha_one_query_row(backend, b, sk, h, kvh, causal):
+    """seqQ = 1 (the reference's decode step after KVPageGather) runs on the paged
+    decode kernels over contiguous K/V: against the oracle's MHA per sequence."""
+    import puter_amd
+    dt, d = O.BF16, 128
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(700 + sk, (b, 1, h * d), 0.0, std), dt)
+    k = encode(seeded(701 + sk, (b, sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(702 + sk, (b, sk, kvh * d)), dt)
+    out = empty_dev((b, 1, h * d), np.uint16)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, 0, 0.0, kvh)
+    if b == 1:
+        backend.MultiHeadAttention(cfg, to_dev(q[0]), to_dev(k[0]), to_dev(v[0]), out, 1, sk, dt)
+    else:
+        backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, 1, sk, dt)
+    got = decode(to_host(out, np.uint16), dt)
+    for i in range(b):
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, dtype=dt), dt)
+        assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"one-row mha sequence {i}")
+
+
 def test_mha_window_alibi(backend):
     import puter_amd
     dt, sq, h, d = O.F32, 40, 2, 32
