@@ -257,10 +257,29 @@ def decode(torch, be, puter, fp8):
     t = Timer(torch).time(fn, 20, warmup=3)
     kv_bytes = int(ctx.sum()) * KV * D * 2 * eb
     name = "fp8" if fp8 else "bf16"
-    return {f"decode_{name}_us": round(t * 1e3, 1),
-            f"decode_{name}_GBs": round(kv_bytes / (t * 1e-3) / 1e9, 1),
-            f"decode_{name}_hbm_frac": round(kv_bytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "decode_sum_ctx": int(ctx.sum())}
+    res = {f"decode_{name}_us": round(t * 1e3, 1),
+           f"decode_{name}_GBs": round(kv_bytes / (t * 1e-3) / 1e9, 1),
+           f"decode_{name}_hbm_frac": round(kv_bytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "decode_sum_ctx": int(ctx.sum())}
+    if not fp8:
+        # the reference's own path for the same step (execution/page_intrinsic.go:277-352
+        # then MultiHeadAttention with one query row, per sequence): KVPageGather of K
+        # and V into contiguous rows, then attention over them
+        kg = torch.empty(maxc * KV * D, device="cuda", dtype=torch.bfloat16)
+        vg = torch.empty_like(kg)
+        mcfg = puter.MultiHeadAttentionConfig(H, D, True, 0, 0.0, KV)
+
+        def ref_path():
+            for i in range(B):
+                c = int(ctx[i])
+                be.KVPageGather(kp, tt[i], kg, total, PS, KV * D, c, 0, fmt)
+                be.KVPageGather(vp, tt[i], vg, total, PS, KV * D, c, 0, fmt)
+                be.MultiHeadAttention(mcfg, q[i * H * D:(i + 1) * H * D], kg, vg,
+                                      out[i * H * D:(i + 1) * H * D], 1, c, fmt)
+        t2 = Timer(torch).time(ref_path, 3, warmup=1)
+        res["decode_bf16_gather_then_mha_us"] = round(t2 * 1e3, 1)
+        del kg, vg
+    return res
 
 
 def matmul_bf16(torch, be, puter):
