@@ -21,8 +21,9 @@
  *     formats with at most 512 rows, F32 outputs of fewer than 256 64x64 tiles)
  *     and puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16, head
  *     dim 128): one buffer per device, allocated on first use and
- *     grown on demand (at most ~16 MB); a growth waits on the host for the
- *     buffer's last user before freeing it.
+ *     grown on demand (Matmul: at most ~16 MB; one-row attention: the paged
+ *     decode workspace size); a growth waits on the host for the buffer's
+ *     last user before freeing it.
  *
  * Status codes follow the reference's CUDA bridge (device/cuda/internal/bridge/status.c):
  *   -2 nil buffer, -6 invalid dtype / shape / config, -7 device unavailable,
