@@ -19,8 +19,8 @@
  *     puter_hip_paged_decode_workspace_bytes).  The one allocation the library
  *     makes itself is a split-K scratch shared by puter_hip_matmul (16-bit
  *     formats with at most 512 rows, F32 outputs of fewer than 256 64x64 tiles)
- *     and puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16, head
- *     dim 128): one buffer per device, allocated on first use and
+ *     and puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16 / f16,
+ *     head dim 128): one buffer per device, allocated on first use and
  *     grown on demand (Matmul: at most ~16 MB; one-row attention: the paged
  *     decode workspace size); a growth waits on the host for the buffer's
  *     last user before freeing it.

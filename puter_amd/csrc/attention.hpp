@@ -20,7 +20,7 @@ struct MhaArgs {
 // MFMA bf16 flash prefill (prefill.hip).  Returns true and sets *status when
 // the shape is one it serves (bf16, head_dim 128, no window / ALiBi).
 bool launch_prefill_mfma(const MhaArgs &a, int dtype, hipStream_t s, int *status);
-// one query row per sequence (bf16, head_dim 128): the paged decode kernels
+// one query row per sequence (bf16 / f16, head_dim 128): the paged decode kernels
 bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *status);
 
 }  // namespace puter

@@ -37,6 +37,7 @@ namespace puter {
 constexpr int kSplit = 256;  // tokens per split (one wave, 8 sub-chunks of 32)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -69,6 +70,18 @@ __device__ __forceinline__ uint4 fp8x8_to_bf16(uint2 raw) {
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// 8 f16 values -> f32 with the hardware widening: exact, and a signalling NaN
+// comes out quiet, which no attention output can tell apart (any NaN in a live
+// row makes the output NaN either way)
+__device__ __forceinline__ void f16x8_to_f32(const uint4 &w, float (&v)[8]) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] & 0xFFFFu));
+        v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
+    }
+}
+
 // One wave per (kv head, 256-token split, sequence): the split is walked in
 // eight 32-token sub-chunks with an online softmax.  Once sub-chunk n's rows
 // have landed and its K rows are parked in LDS, sub-chunk n+1's K and V rows
@@ -83,8 +96,10 @@ template <int KV, int G, int SPLIT = kSplit>
 __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a) {
     constexpr int D = 128, SUB = 32, NSUB = SPLIT / SUB, NGRP = (SPLIT + 63) / 64;
     constexpr bool BF = KV == PUTER_BF16;
-    constexpr int RB = BF ? 256 : 128;            // KV row bytes
-    using VT = typename std::conditional<BF, uint4, uint2>::type;
+    constexpr bool H16 = KV == PUTER_F16;         // f16 K/V and query (one-row attention)
+    constexpr bool W16 = BF || H16;               // 16-bit K/V rows
+    constexpr int RB = W16 ? 256 : 128;           // KV row bytes
+    using VT = typename std::conditional<W16, uint4, uint2>::type;
     __shared__ __attribute__((aligned(1024))) char k_lds[SUB * RB];
     __shared__ float p_lds[SUB][G];               // probabilities [token][head]
 
@@ -102,7 +117,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
     const int64_t head_off = (int64_t)kvh * D;
     const uint8_t *kpool = static_cast<const uint8_t *>(a.kp);
     const uint8_t *vpool = static_cast<const uint8_t *>(a.vp);
-    constexpr int EB = BF ? 2 : 1;
+    constexpr int EB = W16 ? 2 : 1;
     // byte offset of this lane's piece of pool row `row`
     auto piece = [&](int row) -> int64_t { return ((int64_t)row * inner + head_off) * EB + (int64_t)sizeof(VT) * l16; };
 
@@ -139,7 +154,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int64_t off = piece(max(__shfl(src, base + 4 * k + grp, 64), 0));
-            if constexpr (BF) {
+            if constexpr (W16) {
                 kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
                 vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
             } else {
@@ -149,7 +164,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
         }
     };
 
-    const float kscale = BF ? 1.0f : a.ks[kvh];
+    const float kscale = W16 ? 1.0f : a.ks[kvh];
     const float c = a.scale * kscale * 1.4426950408889634f;
     float m_run = -INFINITY, l_run = 0.0f;   // head l16's running max (log2 domain) and sum
     float acc[G][8];
@@ -170,7 +185,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int r = 4 * k + grp;
-            if constexpr (BF) *reinterpret_cast<uint4 *>(k_lds + r * 256 + ((l16 ^ (r & 15)) << 4)) = kbuf[k];
+            if constexpr (W16) *reinterpret_cast<uint4 *>(k_lds + r * 256 + ((l16 ^ (r & 15)) << 4)) = kbuf[k];
             else *reinterpret_cast<uint2 *>(k_lds + r * 128 + ((l16 ^ ((r >> 1) & 7)) << 3)) = kbuf[k];
         }
         if (n + 1 < NSUB) issue(n + 1, kbuf, vbuf[(n + 1) & 1]);
@@ -188,13 +203,17 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 uint4 kv;
-                if constexpr (BF) {
+                if constexpr (W16) {
                     kv = *reinterpret_cast<const uint4 *>(k_lds + row * 256 + (((4 * t + grp) ^ l16) << 4));
                 } else {
                     kv = fp8x8_to_bf16(*reinterpret_cast<const uint2 *>(
                         k_lds + row * 128 + (((4 * t + grp) ^ ((l16 >> 1) & 7)) << 3)));
                 }
-                s[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], s[i], 0, 0, 0);
+                if constexpr (H16)
+                    s[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, kv),
+                                                                  __builtin_bit_cast(f16x8_t, qb[t]), s[i], 0, 0, 0);
+                else
+                    s[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], s[i], 0, 0, 0);
             }
         }
         // lane's scores: head l16, tokens 16i + 4grp + r
@@ -205,6 +224,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
             for (int r = 0; r < 4; ++r) {
                 float v = s[i][r];
                 if constexpr (BF) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
+                if constexpr (H16) v = (float)(_Float16)v;              // f16 dot, likewise (RNE)
                 v = ((liveg >> (16 * i + r)) & 1) ? v * c : -INFINITY;
                 s[i][r] = v;
                 mx = fmaxf(mx, v);
@@ -239,10 +259,11 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
         for (int k = 0; k < 8; ++k) {
             const uint32_t keep = ((livev >> (4 * k)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
             float v[8];
-            if constexpr (BF) {
+            if constexpr (W16) {
                 uint4 w = vc[k];
                 w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
-                unpack_vec<PUTER_BF16>(w, v);
+                if constexpr (H16) f16x8_to_f32(w, v);
+                else unpack_vec<PUTER_BF16>(w, v);
             } else {   // E4M3 widened straight to f32 (the same values as through bf16)
                 const uint32_t w[2] = {vc[k].x & keep, vc[k].y & keep};
 #pragma unroll
@@ -330,8 +351,9 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
         O += po[(int64_t)s * D] * f;
     }
     float r = L > 0.0f ? O / L : 0.0f;
-    if constexpr (KV != PUTER_BF16) r *= a.vs[h / (a.heads / a.kv_heads)];
-    a.out[((int64_t)b * a.heads + h) * D + d] = (uint16_t)f32_to_bf16(r);
+    if constexpr (KV == PUTER_F8E4M3) r *= a.vs[h / (a.heads / a.kv_heads)];
+    if constexpr (KV == PUTER_F16) a.out[((int64_t)b * a.heads + h) * D + d] = Elem<PUTER_F16>::store(r);
+    else a.out[((int64_t)b * a.heads + h) * D + d] = (uint16_t)f32_to_bf16(r);
 }
 
 // An empty pool masks every token: the output is zero.
@@ -349,12 +371,14 @@ using namespace puter;
 namespace puter {
 
 // MultiHeadAttention with one query row per sequence (the reference's decode step:
-// gathered K/V, seqQ 1, typed_compute.go:206-237), bf16, head_dim 128, no window or
-// ALiBi: the paged decode kernels over the contiguous K/V (sequence b's keys are
+// gathered K/V, seqQ 1, typed_compute.go:206-237), bf16 or f16, head_dim 128, no
+// window or ALiBi: the paged decode kernels over the contiguous K/V (sequence b's keys are
 // page b of seq_k rows), partials in the library's scratch.  A causal mask with
 // one query row sees every key (bottom-right alignment), as does no mask.
 bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
-    if (dtype != PUTER_BF16 || m.dim != 128 || m.seq_q != 1 || m.window > 0 || m.alibi != 0.0f) return false;
+    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || m.dim != 128 || m.seq_q != 1 || m.window > 0 ||
+        m.alibi != 0.0f)
+        return false;
     const int64_t G = m.heads / m.kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return false;
     if (!aligned16(m.q) || !aligned16(m.k) || !aligned16(m.v) || !aligned16(m.o)) return false;
@@ -381,23 +405,22 @@ bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *s
                  m.kv_heads, splits, m.seq_k, m.scale};
     const dim3 grid((unsigned)m.kv_heads, (unsigned)splits, (unsigned)m.batch);
     const dim3 cgrid((unsigned)m.heads, (unsigned)m.batch);
-    if (short_splits) {
-        switch (G) {
-        case 1: decode_kernel<PUTER_BF16, 1, 64><<<grid, 64, 0, s>>>(a); break;
-        case 2: decode_kernel<PUTER_BF16, 2, 64><<<grid, 64, 0, s>>>(a); break;
-        case 4: decode_kernel<PUTER_BF16, 4, 64><<<grid, 64, 0, s>>>(a); break;
-        case 8: decode_kernel<PUTER_BF16, 8, 64><<<grid, 64, 0, s>>>(a); break;
-        }
-        decode_combine_kernel<PUTER_BF16, 64><<<cgrid, 128, 0, s>>>(a);
+#define PUTER_ONE_ROW(KVD, SPL)                                                        \
+    switch (G) {                                                                       \
+    case 1: decode_kernel<KVD, 1, SPL><<<grid, 64, 0, s>>>(a); break;                  \
+    case 2: decode_kernel<KVD, 2, SPL><<<grid, 64, 0, s>>>(a); break;                  \
+    case 4: decode_kernel<KVD, 4, SPL><<<grid, 64, 0, s>>>(a); break;                  \
+    case 8: decode_kernel<KVD, 8, SPL><<<grid, 64, 0, s>>>(a); break;                  \
+    }                                                                                  \
+    decode_combine_kernel<KVD, SPL><<<cgrid, 128, 0, s>>>(a);
+    if (dtype == PUTER_BF16) {
+        if (short_splits) { PUTER_ONE_ROW(PUTER_BF16, 64) }
+        else { PUTER_ONE_ROW(PUTER_BF16, kSplit) }
     } else {
-        switch (G) {
-        case 1: decode_kernel<PUTER_BF16, 1><<<grid, 64, 0, s>>>(a); break;
-        case 2: decode_kernel<PUTER_BF16, 2><<<grid, 64, 0, s>>>(a); break;
-        case 4: decode_kernel<PUTER_BF16, 4><<<grid, 64, 0, s>>>(a); break;
-        case 8: decode_kernel<PUTER_BF16, 8><<<grid, 64, 0, s>>>(a); break;
-        }
-        decode_combine_kernel<PUTER_BF16><<<cgrid, 128, 0, s>>>(a);
+        if (short_splits) { PUTER_ONE_ROW(PUTER_F16, 64) }
+        else { PUTER_ONE_ROW(PUTER_F16, kSplit) }
     }
+#undef PUTER_ONE_ROW
     const int rc = check_launch("mha one-row decode");
     const int fin = lease.finish();
     *status = rc ? rc : fin;

@@ -156,17 +156,19 @@ def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
                  elem_tol=1e-3 if dt == O.F32 else None, what="mha")
 
 
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("b,sk,h,kvh,causal", [
     (1, 4096, 32, 8, True),     # configs[4]'s heads at one sequence's full context
     (1, 100, 8, 8, False),      # group size 1, part of one split
     (1, 300, 16, 2, True),      # group size 8
     (3, 700, 8, 4, True),       # batched, partial last split
+    (64, 2000, 32, 8, True),    # 256-token splits (enough waves)
 ])
-def test_mha_one_query_row(backend, b, sk, h, kvh, causal):
+def test_mha_one_query_row(backend, dt, b, sk, h, kvh, causal):
     """seqQ = 1 (the reference's decode step after KVPageGather) runs on the paged
     decode kernels over contiguous K/V: against the oracle's MHA per sequence."""
     import puter_amd
-    dt, d = O.BF16, 128
+    d = 128
     std = 1.0 / np.sqrt(d)
     q = encode(seeded(700 + sk, (b, 1, h * d), 0.0, std), dt)
     k = encode(seeded(701 + sk, (b, sk, kvh * d), 0.0, std), dt)
