@@ -102,6 +102,22 @@ def test_matmul_skinny_two_streams_share_the_scratch_safely(backend):
             assert np.array_equal(to_host(outs[i], np.uint16), alone[i]), (rep, i)
 
 
+def test_matmul_unaligned_16bit_falls_back(backend):
+    """A left operand at an odd element offset is not 16-byte aligned: the MFMA and
+    split-K paths are skipped for the generic kernel, whose result still meets the
+    bar."""
+    import torch
+    rows, inner, cols = 64, 256, 512
+    a = O.from_f32(seeded(971, (rows, inner)), O.BF16)
+    b = O.from_f32(seeded(972, (inner, cols), 0.0, 0.05), O.BF16)
+    abuf = torch.zeros(rows * inner + 1, dtype=torch.int16, device="cuda")
+    abuf[1:] = to_dev(a).view(-1)
+    out = empty_dev((rows, cols), np.uint16)
+    backend.Matmul(out, abuf[1:], to_dev(b), rows, inner, cols, O.BF16)
+    ref = O.to_f32(O.matmul(a, b, O.BF16), O.BF16)
+    assert_close(O.to_f32(to_host(out, np.uint16), O.BF16), ref, TOL[O.BF16], elem_tol=None, what="unaligned")
+
+
 def test_matmul_skinny_k_tail_never_reads_the_next_row(backend):
     """Split-K path: inner = 72 is two chunks of one 64-deep slice each, the second
     holding 8 valid columns; only output row 1 may be NaN."""

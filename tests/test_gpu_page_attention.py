@@ -185,6 +185,26 @@ def test_mha_one_query_row(backend, dt, b, sk, h, kvh, causal):
         assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"one-row mha sequence {i}")
 
 
+def test_mha_one_query_row_unaligned_falls_back(backend):
+    """A query not 16-byte aligned (an odd element offset) cannot take the decode
+    kernels' 16-byte loads: the call falls back to the general kernel and the
+    result still matches the oracle."""
+    import puter_amd
+    import torch
+    dt, h, kvh, d, sk = O.BF16, 8, 2, 128, 300
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(801, (1, h * d), 0.0, std), dt)
+    k = encode(seeded(802, (sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(803, (sk, kvh * d)), dt)
+    qbuf = torch.zeros(h * d + 1, dtype=torch.int16, device="cuda")
+    qbuf[1:] = to_dev(q).view(-1)
+    out = empty_dev((1, h * d), np.uint16)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, True, 0, 0.0, kvh)
+    backend.MultiHeadAttention(cfg, qbuf[1:], to_dev(k), to_dev(v), out, 1, sk, dt)
+    ref = decode(O.mha(q, k, v, h, d, causal=True, kv_heads=kvh, dtype=dt), dt)
+    assert_close(decode(to_host(out, np.uint16), dt), ref, TOL[dt], elem_tol=None, what="unaligned one-row mha")
+
+
 def test_mha_window_alibi(backend):
     import puter_amd
     dt, sq, h, d = O.F32, 40, 2, 32
