@@ -50,16 +50,39 @@ class Timer:
         return s.elapsed_time(e) / iters  # ms
 
 
+class NormPool:
+    """residual / branch / hidden / normed pools of n bf16 elements for the norm
+    sweep.  Each launch of a rows x hidden shape takes the next rows*hidden
+    window of the pools (wrapping at the end), so no launch reads bytes that a
+    recent launch left in the 256 MB last-level cache: every shape is timed from
+    HBM, the small ones included."""
+
+    def __init__(self, torch, n, gen):
+        bf = torch.bfloat16
+        self.n = n
+        self.res = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+        self.br = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+        self.hid = torch.empty(n, device="cuda", dtype=bf)
+        self.out = torch.empty(n, device="cuda", dtype=bf)
+        self.base = [t.data_ptr() for t in (self.res, self.br, self.hid, self.out)]
+        self.cur = 0
+
+    def next(self, count):
+        """Device addresses (res, br, hid, out) of the next count-element window."""
+        if self.cur + count > self.n:
+            self.cur = 0
+        off = 2 * self.cur
+        self.cur += count
+        return [b + off for b in self.base]
+
+
 def norm_sweep(torch, be, puter, steps, warmup):
     """returns (metric dict, dominant-kernel roofline dict)."""
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
     rmax, hmax = max(ROWS), max(HIDDEN)
     n = rmax * hmax
     bf = torch.bfloat16
-    res = torch.randn(n, device="cuda", dtype=bf, generator=gen)
-    br = torch.randn(n, device="cuda", dtype=bf, generator=gen)
-    hid = torch.empty(n, device="cuda", dtype=bf)
-    out = torch.empty(n, device="cuda", dtype=bf)
+    pool = NormPool(torch, n, gen)
     mod = torch.randn(3 * hmax, device="cuda", dtype=bf, generator=gen)
     gamma = 1 + 0.02 * torch.randn(hmax, device="cuda", dtype=torch.float32, generator=gen)
     gamma = gamma.to(bf)
@@ -69,9 +92,11 @@ def norm_sweep(torch, be, puter, steps, warmup):
     for r in ROWS:
         for h in HIDDEN:
             def rms(r=r, h=h):
+                res, br, hid, out = pool.next(r * h)
                 be.GatedResidualRMSNorm(cfg, res, br, mod, gamma, hid, out, r, h, r, 3 * h, 0, puter.BF16)
 
             def ln(r=r, h=h):
+                res, br, hid, out = pool.next(r * h)
                 be.GatedResidualLayerNorm(res, br, mod, gamma, beta, hid, out, r, h, r, 3 * h, 0, puter.BF16)
             launches.append((r, h, "rms", rms))
             launches.append((r, h, "ln", ln))
@@ -96,7 +121,7 @@ def norm_sweep(torch, be, puter, steps, warmup):
     dom_ms = timer.time(dom[3], 50)
     # context, not this library: the same op in eager torch (h = res + gate * branch,
     # y = rms_norm(h)), charged the fused op's 8 B/elem
-    r2, b2, h2 = res.view(rmax, hmax), br.view(rmax, hmax), hid.view(rmax, hmax)
+    r2, b2, h2 = pool.res.view(rmax, hmax), pool.br.view(rmax, hmax), pool.hid.view(rmax, hmax)
     gate, g2 = mod[2 * hmax:3 * hmax], gamma[:hmax]
 
     def torch_gr_rms():
@@ -110,7 +135,7 @@ def norm_sweep(torch, be, puter, steps, warmup):
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "norm_wave_kernel<bf16,RMS,GR,16> (fused gated residual + RMSNorm)",
             "workload": f"{rmax}x{hmax} bf16, {dom_bytes} B/launch", "avg_launch_us": round(dom_ms * 1e3, 2)}
-    del res, br, hid, out
+    del pool, r2, b2, h2
     torch.cuda.empty_cache()
     return ms, step_bytes, per, roof
 
@@ -179,8 +204,9 @@ def rope_swiglu_casts(torch, be, puter):
     return res
 
 
-def prefill(torch, be, puter):
-    """causal GQA prefill bf16, B4 S4096 Hq32 Hkv8 D128."""
+def prefill(torch, be, puter, return_fn=False):
+    """causal GQA prefill bf16, B4 S4096 Hq32 Hkv8 D128 (return_fn:
+    only build the inputs and return the launch)."""
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0003)
     B, S, H, KV, D = 4, 4096, 32, 8, 128
     sc = 1.0 / math.sqrt(D)
@@ -190,6 +216,8 @@ def prefill(torch, be, puter):
     o = torch.empty_like(q)
     cfg = puter.MultiHeadAttentionConfig(H, D, True, 0, 0.0, KV)
     fn = lambda: be.MultiHeadAttentionBatched(cfg, q, k, v, o, B, S, S, puter.BF16)  # noqa: E731
+    if return_fn:
+        return fn
     fn()
     t = Timer(torch).time(fn, 10, warmup=3)
     flops = 4.0 * B * H * D * S * (S + 1) / 2
@@ -216,8 +244,9 @@ def prefill(torch, be, puter):
     return res
 
 
-def decode(torch, be, puter, fp8):
-    """paged decode, B64, ctx ~ U[512, 8192], page 16, Hq32 Hkv8 D128."""
+def decode(torch, be, puter, fp8, return_fn=False):
+    """paged decode, B64, ctx ~ U[512, 8192], page 16, Hq32 Hkv8 D128
+    (return_fn: only build the inputs and return the launch)."""
     import numpy as np
     rng = np.random.default_rng(0x5EED0004)
     B, H, KV, D, PS = 64, 32, 8, 128, 16
@@ -253,6 +282,8 @@ def decode(torch, be, puter, fp8):
     cc = torch.from_numpy(ctx).cuda()
     fn = lambda: be.PagedDecodeAttention(q, kp, vp, tt, cc, B, maxp, PS, total, H, KV, D, maxc, ks, vs, fmt,  # noqa: E731
                                          out, ws, wsb)
+    if return_fn:
+        return fn
     fn()
     t = Timer(torch).time(fn, 20, warmup=3)
     kv_bytes = int(ctx.sum()) * KV * D * 2 * eb
@@ -545,6 +576,36 @@ def profile_matmul(torch, be, puter, launches):
     log(f"profile workload done: {launches} x Matmul bf16 {M}x{K}x{N}")
 
 
+def profile_workload(torch, be, puter, spec, launches):
+    """Counter-collection workloads, one kernel family per run (`--profile-workload
+    NAME --profile-launches N`): `norm:ROWSxHIDDEN` (fused GatedResidual+RMSNorm
+    bf16 on one shape, each launch on the next window of 1 GiB pools so none is
+    served from the 256 MB last-level cache), `prefill`, `decode_bf16` / `decode_fp8`
+    (configs[4]).  Each launch is preceded by nothing else on the stream."""
+    if spec.startswith("norm:"):
+        r, h = (int(x) for x in spec[5:].split("x"))
+        gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
+        pool = NormPool(torch, max(r * h, (1 << 30) // 2), gen)
+        mod = torch.randn(3 * h, device="cuda", dtype=torch.bfloat16, generator=gen)
+        gamma = torch.ones(h, device="cuda", dtype=torch.bfloat16)
+        cfg = puter.RMSNormConfig(1e-5)
+        for _ in range(launches):
+            res, br, hid, out = pool.next(r * h)
+            be.GatedResidualRMSNorm(cfg, res, br, mod, gamma, hid, out, r, h, r, 3 * h, 0, puter.BF16)
+    elif spec == "prefill":
+        fn = prefill(torch, be, puter, return_fn=True)
+        for _ in range(launches):
+            fn()
+    elif spec in ("decode_bf16", "decode_fp8"):
+        fn = decode(torch, be, puter, spec == "decode_fp8", return_fn=True)
+        for _ in range(launches):
+            fn()
+    else:
+        raise SystemExit(f"unknown workload {spec}")
+    torch.cuda.synchronize()
+    log(f"profile workload done: {launches} x {spec}")
+
+
 def measure_traffic():
     """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc
     passes (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) over
@@ -597,6 +658,9 @@ def main():
     ap.add_argument("--only", default="norm,rope,prefill,decode,matmul,block,cpu,traffic")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant kernel N times plus a 1 GiB calibration copy")
+    ap.add_argument("--profile-workload", default="", metavar="NAME",
+                    help="only run one counter-collection workload: norm:RxH, prefill, decode_bf16, decode_fp8")
+    ap.add_argument("--profile-launches", type=int, default=5, metavar="N")
     ap.add_argument("--profile-matmul", type=int, default=0, metavar="N",
                     help="only run the bf16 Matmul 8192^3 N times (counter collection)")
     args = ap.parse_args()
@@ -612,6 +676,9 @@ def main():
         return
     if args.profile_matmul:
         profile_matmul(torch, be, puter, args.profile_matmul)
+        return
+    if args.profile_workload:
+        profile_workload(torch, be, puter, args.profile_workload, args.profile_launches)
         return
     only = set(args.only.split(","))
     ms, step_bytes, per, roof = norm_sweep(torch, be, puter, args.steps, args.warmup)

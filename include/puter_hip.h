@@ -12,9 +12,8 @@
  *     with puter_hip_last_error() giving the message (thread-local);
  *   - zero-sized work returns 0 without launching (device/cpu/layernorm/compute.go:19-21);
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
- *     Launches are asynchronous: no entry point synchronises the host, matching
- *     the zero-host-sync rule the reference's interface documents (one
- *     exception, below);
+ *     Launches are asynchronous: no compute entry point synchronises the host,
+ *     matching the zero-host-sync rule the reference's interface documents;
  *   - the caller owns every buffer (workspaces included, see
  *     puter_hip_paged_decode_workspace_bytes).  The one allocation the library
  *     makes itself is a split-K scratch shared by puter_hip_matmul (16-bit
@@ -22,8 +21,9 @@
  *     and puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16 / f16,
  *     head dim 128): one buffer per device, allocated on first use and
  *     grown on demand (Matmul: at most ~16 MB; one-row attention: the paged
- *     decode workspace size); a growth waits on the host for the buffer's
- *     last user before freeing it.
+ *     decode workspace size).  A growth is stream-ordered on the calling
+ *     stream (hipFreeAsync of the old buffer after its last user, then
+ *     hipMallocAsync): it never blocks the host.
  *
  * Status codes follow the reference's CUDA bridge (device/cuda/internal/bridge/status.c):
  *   -2 nil buffer, -6 invalid dtype / shape / config, -7 device unavailable,
@@ -174,6 +174,14 @@ PUTER_API int puter_hip_multi_axis_rope(const puter_multi_axis_rope_config *conf
                               void *output, int64_t batch, int64_t seq_len, int64_t num_heads,
                               int64_t head_dim, int dtype, void *stream);
 
+/* RoPEPairs(output, input, cosBuffer, sinBuffer, halfDim, format) interface.go:605-609;
+ * device/cpu/rope/ops.go:25-38 -> RopePairsGeneric f32_generic.go:3-11.  F32 only
+ * (any other dtype is PUTER_ERR_INVALID, where the reference panics, ops.go:10-14):
+ * output[2i] = in[2i]*cos[i] - in[2i+1]*sin[i], output[2i+1] = in[2i]*sin[i] +
+ * in[2i+1]*cos[i] for i < half_dim, each operation rounded to f32. */
+PUTER_API int puter_hip_rope_pairs(void *output, const void *input, const void *cos_buffer,
+                                   const void *sin_buffer, int64_t half_dim, int dtype, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* Activation family (gated subset + Silu/Gelu): device/interface.go:18-74   */
 /* ------------------------------------------------------------------------ */
@@ -217,18 +225,28 @@ PUTER_API int puter_hip_cast(void *dst, int dst_dtype, const void *src, int src_
 /* Paged KV: optional hooks execution/page_intrinsic.go:13-24 (called at      */
 /* :199-211 and :334-344).  storage is [pages, pageSize, inner] starting      */
 /* storage_offset elements into the buffer.                                   */
-/* Rows whose page id / offset fall outside the storage are skipped (write)   */
-/* or zero-filled (gather): the device never reads or writes out of bounds.  */
+/*                                                                            */
+/* Ids are validated on the device (the host cannot read them without a      */
+/* synchronisation).  Where the reference's CPU path rejects the whole call   */
+/* with ErrShapeMismatch (device/cpu/shape/page.go:139-146,191-203), a row    */
+/* whose page id or slot is out of range is skipped (write) or zero-filled    */
+/* (gather), no access leaves the storage, and PUTER_ERR_INVALID is stored    */
+/* into *status, a caller-owned 4-byte-aligned device int32 (NULL: not        */
+/* reported).  The library never clears it: the caller zeroes it, reads it at */
+/* its next synchronisation and panics when it is non-zero.                   */
+/* Write order matches the reference's sequential copy: among rows that       */
+/* target one (page, slot) the last row wins (page_generic.go:23-27).         */
 /* ------------------------------------------------------------------------ */
 PUTER_API int puter_hip_kv_page_write(const void *storage, const void *values, const int32_t *page_ids,
                             const int32_t *offsets, void *output, int64_t page_count,
                             int64_t page_size, int64_t inner, int64_t value_rows,
-                            int64_t storage_offset, int dtype, void *stream);
+                            int64_t storage_offset, int dtype, int32_t *status, void *stream);
 /* out_rows must not exceed len(page_table) * page_size: the reference caller caps
  * it there before the call (execution/page_intrinsic.go:326-330). */
 PUTER_API int puter_hip_kv_page_gather(const void *storage, const int32_t *page_table, void *output,
                              int64_t page_count, int64_t page_size, int64_t inner,
-                             int64_t out_rows, int64_t storage_offset, int dtype, void *stream);
+                             int64_t out_rows, int64_t storage_offset, int dtype, int32_t *status,
+                             void *stream);
 
 /* Extension (no reference method): KVPageWrite into an fp8-E4M3 pool with
  * quantisation.  The reference writes rows in the storage dtype
@@ -239,13 +257,13 @@ PUTER_API int puter_hip_kv_page_gather(const void *storage, const int32_t *page_
  * slot offsets[r] of the pool [pages, page_size, kv_heads, head_dim] that starts
  * storage_offset bytes into `storage`.  It is the inverse of the paged decode's
  * dequantisation decode(byte) * scale.  Written in place (the device caller's
- * output == storage, page_intrinsic.go:199-205); rows whose page id or slot is
- * out of range are skipped. */
+ * output == storage, page_intrinsic.go:199-205); out-of-range rows, duplicate
+ * slots and *status as puter_hip_kv_page_write. */
 PUTER_API int puter_hip_kv_page_write_fp8(void *storage, const void *values, const int32_t *page_ids,
                                           const int32_t *offsets, int64_t page_count, int64_t page_size,
                                           int64_t kv_heads, int64_t head_dim, int64_t value_rows,
                                           int64_t storage_offset, const float *scales, int value_dtype,
-                                          void *stream);
+                                          int32_t *status, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Attention: device/interface.go:91-110                                      */
@@ -304,7 +322,8 @@ PUTER_API int puter_hip_flash_attention(const puter_flash_config *config, const 
  * context_lens [batch] int32 (clamped to max_context); num_pages = pool size:
  * a token whose page id is outside [0, num_pages) is masked, never read.
  * workspace: caller-owned device buffer of
- * puter_hip_paged_decode_workspace_bytes(...) bytes. */
+ * puter_hip_paged_decode_workspace_bytes(...) bytes.  query, both pools and
+ * the workspace must be 16-byte aligned (PUTER_ERR_INVALID otherwise). */
 PUTER_API size_t puter_hip_paged_decode_workspace_bytes(int64_t batch, int64_t num_heads,
                                               int64_t head_dim, int64_t max_context);
 PUTER_API int puter_hip_paged_decode_attention(const void *query, const void *key_pages,

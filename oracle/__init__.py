@@ -49,6 +49,11 @@ def lib():
         _lib = C.CDLL(LIBRARY)
         _lib.or_fast_exp32.restype = C.c_float
         _lib.or_fast_exp32.argtypes = [C.c_float]
+        _lib.or_fast_exp64.restype = C.c_double
+        _lib.or_fast_exp64.argtypes = [C.c_double]
+        for name in ("or_fast_tanh32", "or_fast_sigmoid32", "or_fast_silu64"):
+            getattr(_lib, name).restype = C.c_float
+            getattr(_lib, name).argtypes = [C.c_float]
         _lib.or_rmsnorm.argtypes = [C.c_void_p] * 3 + [C.c_int64, C.c_int64, C.c_double, C.c_int]
         _lib.or_layernorm.argtypes = [C.c_void_p] * 4 + [C.c_int64, C.c_int64, C.c_int]
         _lib.or_adaptive_rmsnorm.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 4 + [C.c_double, C.c_int]
@@ -59,6 +64,7 @@ def lib():
                                  C.c_int64, C.c_int64, C.c_int64, C.c_int]
         _lib.or_multi_axis_rope.argtypes = [C.POINTER(MultiAxisRopeConfig), C.c_void_p, C.c_void_p,
                                             C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int]
+        _lib.or_rope_pairs.argtypes = [C.c_void_p] * 4 + [C.c_int64]
         _lib.or_gated_tensors.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int]
         _lib.or_gated_packed.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int]
         _lib.or_unary.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int]
@@ -78,6 +84,7 @@ def lib():
         for name in ("or_dequant_int8", "or_dequant_int4", "or_quant_int8"):
             getattr(_lib, name).argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_float, C.c_int]
         _lib.or_cast_ext.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_size_t]
+        _lib.or_cast_pair.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_size_t]
         _lib.or_matmul.argtypes = [C.c_void_p] * 3 + [C.c_int64] * 3 + [C.c_int]
         _lib.oracle_set_threads.argtypes = [C.c_int]
         _lib.oracle_get_threads.restype = C.c_int
@@ -128,6 +135,27 @@ def from_f32(values: np.ndarray, dtype: int) -> np.ndarray:
 
 def fast_exp32(x: float) -> float:
     return lib().or_fast_exp32(float(x))
+
+
+def fast_exp64(x: float) -> float:
+    """FastExp64 (device/cpu/math/f64.go:10-32)."""
+    return lib().or_fast_exp64(float(x))
+
+
+def fast_tanh32(x: float) -> float:
+    """FastTanh32 (device/cpu/math/f32.go:73-86)."""
+    return lib().or_fast_tanh32(float(x))
+
+
+def fast_sigmoid32(x: float) -> float:
+    """FastSigmoid32 (device/cpu/math/f32.go:88-95)."""
+    return lib().or_fast_sigmoid32(float(x))
+
+
+def fast_silu64(x: float) -> float:
+    """float32(FastSilu64(float64(x))) (device/cpu/math/f64.go:90-92): one entry of
+    the 16-bit Silu tables (device/cpu/activation/lut.go:14-62) before narrowing."""
+    return lib().or_fast_silu64(float(x))
 
 
 # ---- norms ----
@@ -198,6 +226,14 @@ def multi_axis_rope(x, base_freq, latent_seq_len, latent_side, axis_dims, dtype)
     out = np.empty_like(x)
     _check(lib().or_multi_axis_rope(C.byref(cfg), _p(x), _p(out), batch, seq, heads, dim, dtype),
            "multi_axis_rope")
+    return out
+
+
+def rope_pairs(x, cos, sin):
+    """RoPEPairs (f32): x holds 2*len(cos) values."""
+    x = _c(x, np.float32); cos = _c(cos, np.float32); sin = _c(sin, np.float32)
+    out = np.empty_like(x)
+    _check(lib().or_rope_pairs(_p(out), _p(x), _p(cos), _p(sin), cos.size), "rope_pairs")
     return out
 
 
@@ -352,6 +388,18 @@ def cast_ext(src, src_dtype, dst_dtype, count=None):
     n = src.size if count is None else count
     out = np.empty(n, _EXT_NP[dst_dtype])
     _check(lib().or_cast_ext(_p(out), dst_dtype, _p(src), src_dtype, n), "cast_ext")
+    return out
+
+
+_PAIR_NP = {F16: np.uint16, BF16: np.uint16, F8E4M3: np.uint8, F8E5M2: np.uint8, F64: np.float64}
+
+
+def cast_pair(src, src_dtype, dst_dtype):
+    """shape.cast between two float formats without an f32 side
+    (execution/shape_cast_intrinsic.go:56-115): f64 widening, float32(v), narrowing."""
+    src = _c(src, _PAIR_NP[src_dtype])
+    out = np.empty(src.size, _PAIR_NP[dst_dtype])
+    _check(lib().or_cast_pair(_p(out), dst_dtype, _p(src), src_dtype, src.size), "cast_pair")
     return out
 
 

@@ -74,6 +74,7 @@ int or_dequant_int8(float *dst, const int8_t *src, size_t count, float scale, in
 int or_dequant_int4(float *dst, const uint8_t *src, size_t count, float scale, int zero_point);
 int or_quant_int8(int8_t *dst, const float *src, size_t count, float scale, int zero_point);
 int or_cast_ext(void *dst, int dst_dtype, const void *src, int src_dtype, size_t count);
+int or_cast_pair(void *dst, int dst_dtype, const void *src, int src_dtype, size_t count);
 
 /* ---- norm.c ---- */
 int or_rmsnorm(const void *input, const void *scale, void *output,
@@ -117,6 +118,9 @@ int or_multi_axis_rope(const or_multi_axis_rope_config *config, const void *inpu
                        int64_t batch, int64_t seq_len, int64_t num_heads, int64_t head_dim,
                        int dtype);
 
+int or_rope_pairs(float *output, const float *input, const float *cos_buffer, const float *sin_buffer,
+                  int64_t half_dim);
+
 /* ---- activation.c ---- */
 enum { OR_GATE_SWIGLU = 0, OR_GATE_GEGLU = 1, OR_GATE_GEGLU_TANH = 2, OR_GATE_SIGLU = 3,
        OR_GATE_GLU = 4, OR_GATE_REGLU = 5, OR_GATE_LINGLU = 6 };
@@ -125,6 +129,12 @@ int or_gated_tensors(int kind, void *dst, const void *gate, const void *up,
 int or_gated_packed(int kind, void *dst, const void *packed,
                     int64_t batch, int64_t half_count, int dtype);
 int or_unary(int kind, void *dst, const void *src, int64_t count, int dtype);
+/* scalar helpers, exported for the pins: FastExp64, FastTanh32, FastSigmoid32,
+ * float32(FastSilu64(x)) */
+double or_fast_exp64(double x);
+float or_fast_tanh32(float x);
+float or_fast_sigmoid32(float x);
+float or_fast_silu64(float x);
 enum { OR_UNARY_SILU = 0, OR_UNARY_GELU = 1 };
 
 /* ---- page.c ---- */

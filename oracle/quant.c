@@ -109,3 +109,26 @@ int or_cast_ext(void *dst, int dst_dtype, const void *src, int src_dtype, size_t
     }
     return 0;
 }
+
+/* shape.cast between two float formats without an f32 side
+ * (execution/shape_cast_intrinsic.go:56-115): every source value widened to
+ * float64 (convert.BytesToFloat64; exact for bf16 / f16 / fp8 / f64), then
+ * float32(v) narrowed to the target (NewBfloat16FromFloat32(float32(v)),
+ * Fromfloat32(float32(v)), NewF8E4M3/E5M2FromFloat32(float32(v))), or the
+ * float64 kept for an f64 target.  Same format: the input unchanged (:35-41). */
+static int or_float_fmt(int dt) { return dt == OR_F16 || dt == OR_BF16 || dt == OR_F8E4M3 || dt == OR_F8E5M2 || dt == OR_F64; }
+int or_cast_pair(void *dst, int dst_dtype, const void *src, int src_dtype, size_t count) {
+    if (!or_float_fmt(src_dtype) || !or_float_fmt(dst_dtype)) return -6;
+    for (size_t i = 0; i < count; ++i) {
+        double v = src_dtype == OR_F64 ? ((const double *)src)[i] : (double)or_load(src, i, src_dtype);
+        if (dst_dtype == OR_F64) {
+            ((double *)dst)[i] = v;
+        } else if (src_dtype == dst_dtype) {
+            size_t es = dst_dtype == OR_F16 || dst_dtype == OR_BF16 ? 2 : 1;
+            memcpy((char *)dst + i * es, (const char *)src + i * es, es);
+        } else {
+            or_store(dst, i, (float)v, dst_dtype);
+        }
+    }
+    return 0;
+}

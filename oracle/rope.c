@@ -144,3 +144,15 @@ int or_multi_axis_rope(const or_multi_axis_rope_config *config, const void *inpu
     }
     return 0;
 }
+
+/* RoPEPairs: device/cpu/rope/ops.go:25-38 -> RopePairsGeneric f32_generic.go:3-11 */
+int or_rope_pairs(float *output, const float *input, const float *cos_buffer, const float *sin_buffer,
+                  int64_t half_dim) {
+    for (int64_t i = 0; i < half_dim; ++i) {
+        float c = cos_buffer[i], sn = sin_buffer[i];
+        float e = input[2 * i], o = input[2 * i + 1];
+        output[2 * i] = e * c - o * sn;
+        output[2 * i + 1] = e * sn + o * c;
+    }
+    return 0;
+}

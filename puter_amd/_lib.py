@@ -68,15 +68,16 @@ SIGNATURES = {
     "puter_hip_gated_residual_rmsnorm": ([vp] * 6 + [i64] * 4 + [i32, dbl, i32, vp], i32),
     "puter_hip_gated_residual_layernorm": ([vp] * 7 + [i64] * 4 + [i32, i32, vp], i32),
     "puter_hip_rope": ([C.POINTER(RopeConfig), vp, vp, i64, i64, i64, i32, vp], i32),
+    "puter_hip_rope_pairs": ([vp, vp, vp, vp, i64, i32, vp], i32),
     "puter_hip_multi_axis_rope": ([C.POINTER(MultiAxisRopeConfig), vp, vp, i64, i64, i64, i64,
                                    i32, vp], i32),
     "puter_hip_gated_tensors": ([i32, vp, vp, vp, i64, i32, vp], i32),
     "puter_hip_gated_packed": ([i32, vp, vp, i64, i64, i32, vp], i32),
     "puter_hip_unary": ([i32, vp, vp, i64, i32, vp], i32),
     "puter_hip_cast": ([vp, i32, vp, i32, i64, vp], i32),
-    "puter_hip_kv_page_write": ([vp] * 5 + [i64] * 5 + [i32, vp], i32),
-    "puter_hip_kv_page_gather": ([vp] * 3 + [i64] * 5 + [i32, vp], i32),
-    "puter_hip_kv_page_write_fp8": ([vp] * 4 + [i64] * 6 + [vp, i32, vp], i32),
+    "puter_hip_kv_page_write": ([vp] * 5 + [i64] * 5 + [i32, vp, vp], i32),
+    "puter_hip_kv_page_gather": ([vp] * 3 + [i64] * 5 + [i32, vp, vp], i32),
+    "puter_hip_kv_page_write_fp8": ([vp] * 4 + [i64] * 6 + [vp, i32, vp, vp], i32),
     "puter_hip_multi_head_attention": ([C.POINTER(MHAConfig), vp, vp, vp, vp, i64, i64, i32, vp],
                                        i32),
     "puter_hip_multi_head_attention_batched": ([C.POINTER(MHAConfig), vp, vp, vp, vp, i64, i64,

@@ -111,6 +111,27 @@ class Backend:
     def __init__(self, stream=None):
         self.lib = _lib.load()
         self._stream = stream
+        self._status = None   # device int32 status word of the paged-KV hooks
+
+    def _status_word(self):
+        """The backend's device status word (the Go wrapper keeps one per backend):
+        the paged-KV hooks store PUTER_ERR_INVALID into it when a page id or slot
+        is out of range."""
+        if self._status is None:
+            import torch
+            self._status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        return self._status
+
+    def CheckStatus(self):
+        """Synchronise, read and clear the status word; raise PuterError with the
+        reference's ErrShapeMismatch when a paged-KV call since the last check saw
+        an out-of-range page id or slot (device/cpu/shape/page.go:139-146,191-203)."""
+        if self._status is None:
+            return
+        v = int(self._status.item())
+        self._status.zero_()
+        if v != 0:
+            raise PuterError(v, "tensor: shape mismatch (page id or slot out of range)")
 
     # stream: explicit handle, else torch's current stream on the current device
     def stream(self):
@@ -174,6 +195,11 @@ class Backend:
                             config.OriginalContext)
         check(self.lib.puter_hip_rope(C.byref(c), _ptr(input), _ptr(output), seqLen, numHeads,
                                       headDim, format, self.stream()))
+
+    def RoPEPairs(self, output, input, cosBuffer, sinBuffer, halfDim, format):
+        """device/interface.go:605-609 (F32 only, as device/cpu/rope/ops.go:10-14)."""
+        check(self.lib.puter_hip_rope_pairs(_ptr(output), _ptr(input), _ptr(cosBuffer), _ptr(sinBuffer),
+                                            halfDim, format, self.stream()))
 
     def MultiAxisRoPE(self, config, input, output, batch, seqLen, numHeads, headDim, format):
         dims = (C.c_int64 * 4)(config.AxisDim0, config.AxisDim1, config.AxisDim2, config.AxisDim3)
@@ -300,13 +326,14 @@ class Backend:
         check(self.lib.puter_hip_kv_page_write(_ptr(storage), _ptr(values), _ptr(pageIDs),
                                                _ptr(offsets), _ptr(output), pageCount, pageSize,
                                                inner, valueRows, storageOffset, format,
-                                               self.stream()))
+                                               _ptr(self._status_word()), self.stream()))
 
     def KVPageGather(self, storage, pageTable, output, pageCount, pageSize, inner, outRows,
                      storageOffset, format):
         check(self.lib.puter_hip_kv_page_gather(_ptr(storage), _ptr(pageTable), _ptr(output),
                                                 pageCount, pageSize, inner, outRows,
-                                                storageOffset, format, self.stream()))
+                                                storageOffset, format, _ptr(self._status_word()),
+                                                self.stream()))
 
     def KVPageWriteFP8(self, storage, values, pageIDs, offsets, pageCount, pageSize, kvHeads,
                        headDim, valueRows, storageOffset, scales, valueFormat):
@@ -315,7 +342,7 @@ class Backend:
         check(self.lib.puter_hip_kv_page_write_fp8(_ptr(storage), _ptr(values), _ptr(pageIDs),
                                                    _ptr(offsets), pageCount, pageSize, kvHeads,
                                                    headDim, valueRows, storageOffset, _ptr(scales),
-                                                   valueFormat, self.stream()))
+                                                   valueFormat, _ptr(self._status_word()), self.stream()))
 
     # ---- Attention: device/interface.go:91-110 ----
     @staticmethod

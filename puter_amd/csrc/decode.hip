@@ -461,8 +461,10 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     if (!query || !key_pages || !value_pages || !page_table || !context_lens || !output || !workspace)
         return fail(PUTER_ERR_NIL, "paged decode: nil buffer");
     if (kv_dtype == PUTER_F8E4M3 && (!k_scale || !v_scale)) return fail(PUTER_ERR_NIL, "paged decode: fp8 needs scales");
-    if (!aligned16(query) || !aligned16(key_pages) || !aligned16(value_pages))
-        return fail(PUTER_ERR_INVALID, "paged decode: query and pools must be 16-byte aligned");
+    // the split kernel stores float4 partials into the workspace and the combine
+    // kernel reads them back as float2
+    if (!aligned16(query) || !aligned16(key_pages) || !aligned16(value_pages) || !aligned16(workspace))
+        return fail(PUTER_ERR_INVALID, "paged decode: query, pools and workspace must be 16-byte aligned");
     const size_t need = puter_hip_paged_decode_workspace_bytes(batch, num_heads, head_dim, max_context);
     if (workspace_bytes < need) return fail(PUTER_ERR_INVALID, "paged decode: workspace %zu < %zu bytes", workspace_bytes, need);
     const int64_t splits = splits_for(max_context);

@@ -20,6 +20,29 @@ __device__ __forceinline__ float sigmoid32(float v) {  // f32.go:88-95
 __device__ __forceinline__ float silu32(float v) {  // f32.go:97-99
     return __fdiv_rn(v, __fadd_rn(1.0f, fast_exp32(-v)));
 }
+// FastExp64 (device/cpu/math/f64.go:10-32): FastExp32's 2^f polynomial in
+// float64, scaled by an exact ldexp.  The reference's 16-bit Silu is not
+// FastSilu32: it looks the input up in a 65536-entry table filled with
+// narrow(float32(FastSilu64(x))) (device/cpu/activation/lut.go:14-62,
+// math/f64.go:90-92), so the 16-bit unary Silu runs in float64 here.
+__device__ __forceinline__ double fast_exp64(double x) {
+    if (x < -708.3964185322641) return 0.0;
+    if (x > 709.782712893384) return 1.7976931348623157e308;
+    const double z = __dmul_rn(x, 1.4426950408889634);
+    int64_t k = (int64_t)z;
+    if (z < 0) k--;
+    const double f = __dsub_rn(z, (double)k);
+    double p = __dmul_rn(f, 0.001333899727232439);
+    p = __dmul_rn(f, __dadd_rn(0.009618127167766223, p));
+    p = __dmul_rn(f, __dadd_rn(0.05550410706910451, p));
+    p = __dmul_rn(f, __dadd_rn(0.2402265069591007, p));
+    p = __dmul_rn(f, __dadd_rn(0.6931471805599453, p));
+    return ldexp(__dadd_rn(1.0, p), (int)k);
+}
+__device__ __forceinline__ float silu64(float v) {  // float32(FastSilu64(float64(v)))
+    const double x = (double)v;
+    return (float)__ddiv_rn(x, __dadd_rn(1.0, fast_exp64(-x)));
+}
 __device__ __forceinline__ float gelu32(float v) {  // activation.go:54-57
     const double x = (double)v;
     return (float)(0.5 * x * (1.0 + erf(x * 0.7071067811865475)));
@@ -122,8 +145,13 @@ __global__ __launch_bounds__(256) void unary_kernel(void *__restrict__ dst,
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
         const float v = Elem<DT>::load(reinterpret_cast<const T *>(src)[i]);
-        reinterpret_cast<T *>(dst)[i] =
-            Elem<DT>::store(KIND == PUTER_UNARY_SILU ? silu32(v) : gelu32(v));
+        // f32: FastSilu32 / FastGelu32 (activation/f32_generic.go:72-97); 16-bit: the
+        // reference's table entries, float32(FastSilu64 / FastGelu64) narrowed
+        // (FastGelu64 in float64 then float32 is gelu32's own arithmetic)
+        float y;
+        if constexpr (KIND == PUTER_UNARY_SILU) y = DT == PUTER_F32 ? silu32(v) : silu64(v);
+        else y = gelu32(v);
+        reinterpret_cast<T *>(dst)[i] = Elem<DT>::store(y);
     }
 }
 

@@ -533,9 +533,10 @@ __global__ __launch_bounds__(256) void matmul_splitk_reduce_kernel(uint16_t *c, 
 // Split-K partials: one scratch buffer per device, kept for the life of the
 // process and grown on demand.  A call on another stream than the buffer's last
 // user first waits (on the device, hipStreamWaitEvent) for that user's
-// completion event, so calls on different streams never overlap on the buffer
-// and nothing waits on the host except a growth, which lets the last user finish
-// before the old buffer is freed.  The mutex is held from acquisition until the
+// completion event, so calls on different streams never overlap on the buffer.
+// Nothing waits on the host: a growth frees the old buffer and allocates the new
+// one in stream order on the calling stream (hipFreeAsync / hipMallocAsync),
+// after the last user's work.  The mutex is held from acquisition until the
 // call's launches and event are enqueued.
 struct SplitScratch {
     std::mutex mu;
@@ -554,13 +555,14 @@ static int scratch_acquire(SplitScratch &sc, size_t need, hipStream_t s) {
         return fail(PUTER_ERR_LAUNCH, "matmul: cannot order the split-K scratch");
     if (sc.bytes < need) {
         if (sc.ptr) {
-            if (hipEventSynchronize(sc.done) != hipSuccess || hipFree(sc.ptr) != hipSuccess)
+            // s is ordered after the last user (above, or it is that user)
+            if (hipFreeAsync(sc.ptr, s) != hipSuccess)
                 return fail(PUTER_ERR_LAUNCH, "matmul: cannot release the split-K scratch");
             sc.ptr = nullptr;
             sc.bytes = 0;
         }
         const size_t grown = (need + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
-        if (hipMalloc(&sc.ptr, grown) != hipSuccess) {
+        if (hipMallocAsync(&sc.ptr, grown, s) != hipSuccess) {
             sc.ptr = nullptr;
             return fail(PUTER_ERR_UNAVAILABLE, "matmul: split-K scratch of %zu bytes unavailable", grown);
         }

@@ -78,45 +78,6 @@ __device__ __forceinline__ uint32_t f32_to_i8(float v) {
     if (v != v) return 0u;
     return (uint32_t)(int)v & 0xFFu;  // truncation toward zero
 }
-__device__ __forceinline__ uint64_t f32_to_f64_bits(uint32_t x) {
-    const uint64_t sign = (uint64_t)(x & 0x80000000u) << 32;
-    const uint32_t e = (x >> 23) & 0xFFu, m = x & 0x7FFFFFu;
-    if (e == 0xFFu) {
-        if (m == 0) return sign | 0x7FF0000000000000ull;
-        return sign | 0x7FF8000000000000ull | ((uint64_t)m << 29);  // quiet, payload kept
-    }
-    if (e == 0) {
-        if (m == 0) return sign;
-        const int p = 31 - __clz(m);                                 // top set bit of the denormal
-        return sign | ((uint64_t)(p + 874) << 52) | (((uint64_t)m << (52 - p)) & 0xFFFFFFFFFFFFFull);
-    }
-    return sign | ((uint64_t)(e + 896) << 52) | ((uint64_t)m << 29);
-}
-__device__ __forceinline__ uint32_t f64_to_f32_bits(uint64_t x) {
-    const uint32_t sign = (uint32_t)(x >> 32) & 0x80000000u;
-    const int e = (int)((x >> 52) & 0x7FF);
-    const uint64_t m = x & 0xFFFFFFFFFFFFFull;
-    if (e == 0x7FF) {
-        if (m == 0) return sign | 0x7F800000u;
-        return sign | 0x7FC00000u | (uint32_t)(m >> 29);  // quiet, top payload bits
-    }
-    if (e == 0) return sign;  // f64 denormals lie far below half the least f32 denormal
-    int exp = e - 896;        // biased f32 exponent of the value before rounding
-    if (exp >= 0xFF) return sign | 0x7F800000u;
-    const uint64_t sig = m | (1ull << 52);
-    int shift = 29;
-    if (exp < 1) {
-        shift = 30 - exp;     // gradual underflow: fewer significant bits kept
-        if (shift > 54) return sign;
-    }
-    uint64_t keep = sig >> shift;
-    const uint64_t rem = sig & ((1ull << shift) - 1), half = 1ull << (shift - 1);
-    if (rem > half || (rem == half && (keep & 1))) ++keep;   // round to nearest even
-    if (exp < 1) return sign | (uint32_t)keep;               // 2^23 becomes the least normal
-    if (keep >> 24) { keep >>= 1; ++exp; }
-    if (exp >= 0xFF) return sign | 0x7F800000u;
-    return sign | ((uint32_t)exp << 23) | ((uint32_t)keep & 0x7FFFFFu);
-}
 
 // ---- conversions as unit / element operations ------------------------------
 struct DequantI8Op {  // also Int8ToFloat32 (scale 1, zero point 0: exact)

@@ -363,6 +363,46 @@ __global__ __launch_bounds__(256) void multi_axis_rope_kernel(MultiAxisArgs a) {
     }
 }
 
+// RoPEPairs (device/interface.go:605-609, device/cpu/rope/ops.go:25-38,
+// RopePairsGeneric f32_generic.go:3-11): f32 only; pair i of `input` rotated by
+// (cos[i], sin[i]): out[2i] = e*c - o*s, out[2i+1] = e*s + o*c, each product and
+// difference rounded on its own (no contraction).  Two pairs per thread as one
+// 16-byte input vector and two 8-byte cos / sin reads when the buffers allow.
+__global__ __launch_bounds__(256) void rope_pairs_kernel(float *__restrict__ out, const float *__restrict__ in,
+                                                         const float *__restrict__ cosb,
+                                                         const float *__restrict__ sinb, int64_t pairs,
+                                                         int vectorised) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    auto rot = [](float e, float o, float c, float sn, float &re, float &ro) __attribute__((always_inline)) {
+        re = __fsub_rn(__fmul_rn(e, c), __fmul_rn(o, sn));
+        ro = __fadd_rn(__fmul_rn(e, sn), __fmul_rn(o, c));
+    };
+    if (vectorised) {
+        const int64_t units = pairs / 2;
+        for (int64_t u = first; u < units; u += stride) {
+            const float4 x = reinterpret_cast<const float4 *>(in)[u];
+            const float2 c = reinterpret_cast<const float2 *>(cosb)[u];
+            const float2 sn = reinterpret_cast<const float2 *>(sinb)[u];
+            float4 y;
+            rot(x.x, x.y, c.x, sn.x, y.x, y.y);
+            rot(x.z, x.w, c.y, sn.y, y.z, y.w);
+            reinterpret_cast<float4 *>(out)[u] = y;
+        }
+        if (first == 0 && (pairs & 1)) {
+            const int64_t p = pairs - 1;
+            rot(in[2 * p], in[2 * p + 1], cosb[p], sinb[p], out[2 * p], out[2 * p + 1]);
+        }
+        return;
+    }
+    for (int64_t p = first; p < pairs; p += stride) {
+        float re, ro;
+        rot(in[2 * p], in[2 * p + 1], cosb[p], sinb[p], re, ro);
+        out[2 * p] = re;
+        out[2 * p + 1] = ro;
+    }
+}
+
 template <int DT>
 static int launch_rope(RopeArgs a, hipStream_t s) {
     constexpr int N = Vec<DT>::N;
@@ -440,6 +480,24 @@ int puter_hip_rope(const puter_rope_config *config, const void *input, void *out
     case PUTER_F16: return launch_rope<PUTER_F16>(a, s);
     }
     return PUTER_ERR_INVALID;
+}
+
+int puter_hip_rope_pairs(void *output, const void *input, const void *cos_buffer, const void *sin_buffer,
+                         int64_t half_dim, int dtype, void *stream) {
+    if (half_dim < 0) return fail(PUTER_ERR_INVALID, "rope pairs: negative half_dim");
+    // requireRoPEFloat32 device/cpu/rope/ops.go:10-14
+    if (dtype != PUTER_F32) return fail(PUTER_ERR_INVALID, "rope pairs: unsupported dtype %d", dtype);
+    if (half_dim == 0) return PUTER_OK;
+    if (!output || !input || !cos_buffer || !sin_buffer) return fail(PUTER_ERR_NIL, "rope pairs: nil buffer");
+    const int vec = aligned16(output) && aligned16(input) &&
+                    ((reinterpret_cast<uintptr_t>(cos_buffer) | reinterpret_cast<uintptr_t>(sin_buffer)) & 7u) == 0;
+    const int64_t units = vec ? (half_dim + 1) / 2 : half_dim;
+    int64_t blocks = (units + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    rope_pairs_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+        static_cast<float *>(output), static_cast<const float *>(input), static_cast<const float *>(cos_buffer),
+        static_cast<const float *>(sin_buffer), half_dim, vec);
+    return check_launch("rope pairs");
 }
 
 int puter_hip_multi_axis_rope(const puter_multi_axis_rope_config *config, const void *input,

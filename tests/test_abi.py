@@ -76,13 +76,23 @@ def test_rope_validation(lib):
 
 
 def test_cast_activation_page_validation(lib):
-    assert lib.puter_hip_cast(FAKE, 2, FAKE, 1, 16, None) == _lib.ERR_INVALID      # f16 -> bf16: no f32 side
+    assert lib.puter_hip_cast(FAKE, 2, FAKE, 5, 16, None) == _lib.ERR_INVALID      # int32 -> bf16
+    assert lib.puter_hip_cast(FAKE, 1, FAKE, 6, 16, None) == _lib.ERR_INVALID      # int8 -> f16: no f32 side
     assert lib.puter_hip_cast(None, 0, FAKE, 2, 16, None) == _lib.ERR_NIL
     assert lib.puter_hip_cast(None, 0, None, 2, 0, None) == _lib.OK
     assert lib.puter_hip_gated_tensors(9, FAKE, FAKE, FAKE, 16, 0, None) == _lib.ERR_INVALID
     assert lib.puter_hip_gated_packed(0, FAKE, FAKE, 2, 8, 3, None) == _lib.ERR_INVALID
-    assert lib.puter_hip_kv_page_write(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 0, 8, 2, 0, 0, None) == _lib.ERR_INVALID
-    assert lib.puter_hip_kv_page_gather(FAKE, FAKE, FAKE, 4, 16, 8, 2, 0, 9, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_kv_page_write(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 0, 8, 2, 0, 0, None, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_kv_page_gather(FAKE, FAKE, FAKE, 4, 16, 8, 2, 0, 9, None, None) == _lib.ERR_INVALID
+    # the device status word must be a 4-byte aligned int32
+    assert lib.puter_hip_kv_page_write(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 16, 8, 2, 0, 0, FAKE + 2, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_kv_page_gather(FAKE, FAKE, FAKE, 4, 16, 8, 2, 0, 0, FAKE + 1, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_kv_page_write_fp8(FAKE, FAKE, FAKE, FAKE, 4, 16, 2, 128, 2, 0, FAKE, 2, FAKE + 2,
+                                           None) == _lib.ERR_INVALID
+    # RoPEPairs is F32 only (device/cpu/rope/ops.go:10-14); zero pairs is a no-op
+    assert lib.puter_hip_rope_pairs(FAKE, FAKE, FAKE, FAKE, 8, 2, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_rope_pairs(None, None, None, None, 0, 0, None) == _lib.OK
+    assert lib.puter_hip_rope_pairs(None, FAKE, FAKE, FAKE, 8, 0, None) == _lib.ERR_NIL
 
 
 def test_attention_validation(lib):

@@ -40,9 +40,6 @@ def test_page_write_gather_roundtrip(backend, dt, inner):
     rows = 37
     ids = rng.integers(0, pages, rows).astype(np.int32)
     offs = rng.integers(0, ps, rows).astype(np.int32)
-    # distinct slots so the write order cannot matter
-    slots = np.unique(ids.astype(np.int64) * ps + offs, return_index=True)[1]
-    ids, offs = ids[slots], offs[slots]
     vals = rng.integers(0, 200, size=ids.size * inner).astype(NP[dt] if es < 4 else np.float32)
     ref_store = O.page_write(storage, vals, ids, offs, ps, inner)
     d_store = to_dev(storage)
@@ -94,6 +91,7 @@ def test_page_write_fp8_matches_oracle(backend, dt):
 
 
 def test_page_write_fp8_roundtrip_and_bounds(backend):
+    import puter_amd
     """Dequantised pool rows equal the values within E4M3's half-ulp (2^-4 relative
     for normal codes); rows with a bad page id or slot leave the pool untouched."""
     rng = np.random.default_rng(7)
@@ -112,6 +110,8 @@ def test_page_write_fp8_roundtrip_and_bounds(backend):
     touched = np.zeros((pages, ps), bool)
     touched[3, 2] = touched[5, 15] = True
     assert not got[~touched].any(), "an out-of-range row was written"
+    with pytest.raises(puter_amd.PuterError):      # the status word reports the rejected rows
+        backend.CheckStatus()
     xs = decode(vals, O.BF16)
     for r, (pg, sl) in ((0, (3, 2)), (2, (5, 15))):
         deq = O.to_f32(got[pg, sl], O.F8E4M3).reshape(kvh, hd) * scales[:, None]
@@ -120,17 +120,75 @@ def test_page_write_fp8_roundtrip_and_bounds(backend):
 
 
 def test_page_out_of_range_ids_never_touch_memory(backend):
+    """Where the reference rejects the call (device/cpu/shape/page.go:139-146,191-203)
+    the device path skips (write) or zero-fills (gather) the bad rows, never
+    touches memory outside the storage, and reports through the status word."""
+    import puter_amd
+    backend.CheckStatus()
     pages, ps, inner = 4, 2, 8
     storage = seeded(4, (pages * ps * inner,))
     d = to_dev(storage)
-    backend.KVPageWrite(d, to_dev(np.ones(2 * inner, np.float32)), to_dev(np.array([9, -1], np.int32)),
-                        to_dev(np.array([0, 0], np.int32)), d, pages, ps, inner, 2, 0, O.F32)
-    assert np.array_equal(to_host(d, np.float32), storage)   # both rows skipped
+    vals = seeded(5, (4, inner))
+    ids, offs = np.array([9, 1, -1, 2], np.int32), np.array([0, 1, 0, 2], np.int32)   # rows 0, 2, 3 bad
+    backend.KVPageWrite(d, to_dev(vals), to_dev(ids), to_dev(offs), d, pages, ps, inner, 4, 0, O.F32)
+    with pytest.raises(puter_amd.PuterError) as e:
+        backend.CheckStatus()
+    assert e.value.status == -6
+    want = O.page_write(storage, vals[1:2], ids[1:2], offs[1:2], ps, inner)   # only the valid row landed
+    assert np.array_equal(to_host(d, np.float32), want)
+    backend.CheckStatus()                                     # cleared by the read
     out = empty_dev((2 * ps, inner), np.float32)
     backend.KVPageGather(d, to_dev(np.array([1, 77], np.int32)), out, pages, ps, inner, 2 * ps, 0, O.F32)
     got = to_host(out, np.float32)
-    assert np.array_equal(got[:ps].ravel(), storage[ps * inner:2 * ps * inner])
+    assert np.array_equal(got[:ps].ravel(), want[ps * inner:2 * ps * inner])
     assert np.all(got[ps:] == 0)
+    with pytest.raises(puter_amd.PuterError):
+        backend.CheckStatus()
+    # a valid call leaves the word clear
+    backend.KVPageGather(d, to_dev(np.array([1, 3], np.int32)), out, pages, ps, inner, 2 * ps, 0, O.F32)
+    backend.CheckStatus()
+
+
+@pytest.mark.parametrize("dt,inner,rows", [(O.BF16, 1024, 300), (O.F32, 3, 77), (O.F8E4M3, 1024, 200),
+                                           (O.F16, 5, 1000)])
+def test_page_write_duplicate_slots_last_row_wins(backend, dt, inner, rows):
+    """Rows aimed at the same (page, slot): the reference copies rows in order,
+    so the last one wins (device/cpu/shape/page_generic.go:23-27).  Ids and slots
+    drawn from a small range so most slots are hit several times; every value
+    row distinct, so the pool shows which row landed."""
+    backend.CheckStatus()
+    rng = np.random.default_rng(rows + inner)
+    pages, ps = 6, 4
+    es = np.dtype(NP[dt]).itemsize
+    storage = np.zeros(pages * ps * inner, NP[dt])
+    ids = rng.integers(0, 3, rows).astype(np.int32)
+    offs = rng.integers(0, ps, rows).astype(np.int32)
+    assert np.unique(ids * ps + offs).size < rows // 4
+    vals = (np.arange(rows * inner) % (2**(8 * min(es, 2)) - 3) + 1).astype(NP[dt]) if es < 4 else \
+        np.arange(rows * inner, dtype=np.float32)
+    ref = O.page_write(storage, vals, ids, offs, ps, inner)
+    d = to_dev(storage)
+    backend.KVPageWrite(d, to_dev(vals), to_dev(ids), to_dev(offs), d, pages, ps, inner, rows, 0, dt)
+    assert np.array_equal(to_host(d, storage.dtype).view(np.uint8), ref.view(np.uint8))
+    backend.CheckStatus()
+
+
+def test_page_write_fp8_duplicate_slots_last_row_wins(backend):
+    backend.CheckStatus()
+    rng = np.random.default_rng(11)
+    pages, ps, kvh, hd, rows = 4, 16, 2, 128, 500
+    inner = kvh * hd
+    ids = rng.integers(0, 2, rows).astype(np.int32)
+    offs = rng.integers(0, ps, rows).astype(np.int32)
+    scales = np.array([0.25, 2.0], np.float32)
+    vals = encode(rng.normal(0, 1, (rows, inner)).astype(np.float32), O.BF16)
+    storage = np.zeros(pages * ps * inner, np.uint8)
+    ref = O.page_write_fp8(storage, vals, ids, offs, ps, kvh, hd, scales, O.BF16)
+    d = to_dev(storage)
+    backend.KVPageWriteFP8(d, to_dev(vals), to_dev(ids), to_dev(offs), pages, ps, kvh, hd, rows, 0,
+                           to_dev(scales), O.BF16)
+    assert np.array_equal(to_host(d, np.uint8), ref)
+    backend.CheckStatus()
 
 
 # -------------------------------------------------------------- attention --
@@ -376,6 +434,21 @@ def test_paged_decode_empty_pool(backend):
     pool = np.zeros((1, ps, kvh, d), np.uint16)   # a valid buffer the kernel must not depend on
     out = run_paged_decode(backend, q, pool, pool, table, ctx, ps, 0, h, kvh, d, O.BF16, None, None)
     assert not out.any()
+
+
+def test_paged_decode_rejects_misaligned_workspace(backend):
+    """The split partials are stored as 16-byte vectors: a workspace view that is
+    not 16-byte aligned is rejected before any launch."""
+    import puter_amd
+    h, kvh, d, ps = 8, 2, 128, 16
+    ctx, table, total, q, kp, vp, _, _ = paged_case(8301, 2, 20, 40, ps, h, kvh, d, O.BF16)
+    ws_bytes = backend.PagedDecodeWorkspaceBytes(2, h, d, int(ctx.max()))
+    ws = empty_dev((ws_bytes // 4 + 4,), np.float32)
+    out = empty_dev((2, h * d), np.uint16)
+    with pytest.raises(puter_amd.PuterError):
+        backend.PagedDecodeAttention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(table), to_dev(ctx), 2,
+                                     table.shape[1], ps, total, h, kvh, d, int(ctx.max()), None, None,
+                                     O.BF16, out, ws[1:], ws_bytes)
 
 
 def test_matmul_f32(backend):

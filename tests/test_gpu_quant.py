@@ -132,3 +132,44 @@ def test_quant_errors(backend):
     with pytest.raises(P.PuterError):
         backend.Cast(a, P.I4, b, P.F32, 16)                                     # int4 only as a source
     backend.Quant(b, a, 0, P.DequantInt8Config(1.0, 0), P.I8, P.F32)            # zero count: no-op
+
+
+# ------------------------------ shape.cast between float formats, one launch --
+PAIR_NP = {O.F16: np.uint16, O.BF16: np.uint16, O.F8E4M3: np.uint8, O.F8E5M2: np.uint8, O.F64: np.float64}
+PAIR_FORMATS = [O.BF16, O.F16, O.F8E4M3, O.F8E5M2, O.F64]
+
+
+def _pair_source(dt, n, seed):
+    rng = np.random.default_rng(seed)
+    if dt == O.F64:
+        v = np.concatenate([rng.standard_normal(n) * 300.0, [1 + 2**-8 + 2**-30, np.inf, -np.inf, np.nan,
+                                                            0.0, -0.0, 1e-39, 1e300, 5e-324]])
+        return v[:n].astype(np.float64) if n < 9 else v
+    es = np.dtype(PAIR_NP[dt]).itemsize
+    return rng.integers(0, 1 << (8 * es), n).astype(PAIR_NP[dt])   # every bit pattern class
+
+
+@pytest.mark.parametrize("src", PAIR_FORMATS)
+@pytest.mark.parametrize("dst", PAIR_FORMATS)
+@pytest.mark.parametrize("n,off", [(1, 0), (13, 0), (4096, 0), ((1 << 18) + 5, 0), (1000, 1)])
+def test_cast_float_pair(backend, src, dst, n, off):
+    """Any two of bf16 / f16 / fp8 / f64 in one pass (execution/shape_cast_intrinsic.go:56-115),
+    bit-exact against the oracle (NaN codes compared as NaN), aligned and unaligned."""
+    x = _pair_source(src, n, 100 * src + dst + n)
+    n = x.size
+    ref = x.copy() if src == dst else O.cast_pair(x, src, dst)
+    out_np = PAIR_NP[dst]
+    if off:
+        d_out = to_dev(np.zeros(n + off, out_np))[off:]
+        d_in = _dev_slice(x, off)
+    else:
+        d_out, d_in = empty_dev((n,), out_np), to_dev(x)
+    backend.Cast(d_out, dst, d_in, src, n)
+    got = to_host(d_out, out_np)
+    if dst == O.F64:
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan) and _bits_equal(got[~nan], ref[~nan])
+    else:
+        nan = np.isnan(O.to_f32(ref, dst))
+        assert np.array_equal(np.isnan(O.to_f32(got, dst)), nan)
+        assert np.array_equal(got[~nan], ref[~nan])

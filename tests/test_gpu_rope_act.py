@@ -42,15 +42,22 @@ def test_rope_llama3_in_place(backend):
     assert_close(to_host(t, np.float32), ref, TOL[dt], what="rope llama3")
 
 
-def test_multi_axis_rope(backend):
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16])
+@pytest.mark.parametrize("b,s,h,base,latent,side,dims", [
+    (2, 20, 3, 1e4, 12, 4, [4, 6, 6]),            # 3 axes, 3x4 image grid after 8 text tokens
+    (2, 23, 3, 1e4, 15, 6, [2, 6, 4, 4]),          # 4 axes: text on axis 3, ragged last image row
+    (1, 5, 2, 1e4, 12, 4, [4, 4, 8]),              # every token an image token
+    (1, 640, 4, 1e4, 512, 32, [32, 32, 32, 32]),   # multi_axis_test.go:48-60 scaled down
+])
+def test_multi_axis_rope(backend, dt, b, s, h, base, latent, side, dims):
     import puter_amd
-    for dt in (O.F32, O.BF16):
-        x = encode(seeded(31, (2, 20, 3, 16)), dt)
-        ref = decode(O.multi_axis_rope(x, 1e4, 12, 4, [4, 6, 6], dt), dt)
-        out = empty_dev(x.shape, NP[dt])
-        cfg = puter_amd.MultiAxisRoPEConfig(1e4, 12, 4, 3, 4, 6, 6, 0)
-        backend.MultiAxisRoPE(cfg, to_dev(x), out, 2, 20, 3, 16, dt)
-        assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], what="multi-axis")
+    d = sum(dims)
+    x = encode(seeded(31 + s, (b, s, h, d)), dt)
+    ref = decode(O.multi_axis_rope(x, base, latent, side, dims, dt), dt)
+    out = empty_dev(x.shape, NP[dt])
+    cfg = puter_amd.MultiAxisRoPEConfig(base, latent, side, len(dims), *(list(dims) + [0] * (4 - len(dims))))
+    backend.MultiAxisRoPE(cfg, to_dev(x), out, b, s, h, d, dt)
+    assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], what="multi-axis")
 
 
 GATES = ["SwiGLU", "GeGLU", "GeGLUTanh", "SiGLU", "GLU", "ReGLU", "LinGLU"]
@@ -97,11 +104,59 @@ def test_fast_exp_edges_through_swiglu(backend):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (got, ref)
 
 
-@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16])
 def test_unary_silu_gelu(backend, dt):
-    x = encode(seeded(60, (5000,), 0.0, 4.0), dt)
+    """f32: FastSilu32 bit-exact, FastGelu32 (float64 erf) to the f32 bar.
+    f16 / bf16: every one of the 65536 input patterns, as the reference's
+    tables hold them: Silu = narrow(float32(FastSilu64(x))) bit-exact; Gelu's
+    float64 erf (the device library's vs libm's) may differ in the last f64
+    bits, so at most one 16-bit step on a handful of inputs."""
+    if dt == O.F32:
+        x = encode(seeded(60, (5000,), 0.0, 4.0), dt)
+    else:
+        x = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
     for kind, name in ((O.UNARY_SILU, "Silu"), (O.UNARY_GELU, "Gelu")):
-        ref = decode(O.unary(kind, x, dt), dt)
+        ref = O.unary(kind, x, dt)
         out = empty_dev(x.shape, NP[dt])
         getattr(backend, name)(out, to_dev(x), x.size, dt)
-        assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], what=name)
+        got = to_host(out, NP[dt])
+        if dt == O.F32:
+            if kind == O.UNARY_SILU:
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name
+            else:
+                assert_close(got, ref, TOL[dt], what=name)
+            continue
+        fin = ~np.isnan(decode(ref, dt))
+        nan_ok = np.array_equal(np.isnan(decode(got, dt)), np.isnan(decode(ref, dt)))
+        assert nan_ok, name
+        if kind == O.UNARY_SILU:
+            assert np.array_equal(got[fin], ref[fin]), name
+        else:
+            steps = np.abs(got[fin].astype(np.int64) - ref[fin].astype(np.int64))
+            assert np.max(steps) <= 1 and np.count_nonzero(steps) <= 16, (name, np.count_nonzero(steps))
+
+
+@pytest.mark.parametrize("half", [1, 7, 64, 1024, 8192, 4097])
+def test_rope_pairs(backend, half):
+    """RoPEPairs (device/interface.go:605-609), f32, bit-exact against the oracle's
+    RopePairsGeneric restatement (parity.Lengths of the reference's pair tests)."""
+    x = seeded(70 + half, (2 * half,))
+    ang = seeded(71 + half, (half,), 0.0, 3.0).astype(np.float64)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    ref = O.rope_pairs(x, cos, sin)
+    out = empty_dev((2 * half,), np.float32)
+    backend.RoPEPairs(out, to_dev(x), to_dev(cos), to_dev(sin), half, O.F32)
+    assert np.array_equal(to_host(out, np.float32).view(np.uint32), ref.view(np.uint32))
+    # unaligned views take the element-wise path
+    xd, cd, sd = to_dev(np.concatenate([[0.0], x]).astype(np.float32)), to_dev(cos), to_dev(sin)
+    out2 = empty_dev((2 * half + 1,), np.float32)
+    backend.RoPEPairs(out2[1:], xd[1:], cd, sd, half, O.F32)
+    assert np.array_equal(to_host(out2, np.float32)[1:].view(np.uint32), ref.view(np.uint32))
+
+
+def test_rope_pairs_rejects_16bit(backend):
+    import puter_amd
+    x = empty_dev((8,), np.uint16)
+    c = empty_dev((4,), np.float32)
+    with pytest.raises(puter_amd.PuterError):
+        backend.RoPEPairs(x, x, c, c, 4, O.BF16)   # rope/ops.go:10-14 panics for non-f32

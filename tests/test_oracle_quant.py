@@ -149,3 +149,54 @@ def test_f32_to_f64_exact_and_nan_quieting():
     x = x[np.isfinite(x)]
     back = O.cast_ext(O.cast_ext(x, O.F32, O.F64), O.F64, O.F32)
     assert np.array_equal(back.view(np.uint32), x.view(np.uint32))
+
+
+# ------------------------------------------- shape.cast between float formats --
+def _all16(dtype):
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    return bits[~np.isnan(O.to_f32(bits, dtype))]
+
+
+def test_cast_pair_16bit_each_way_matches_torch():
+    """bf16 <-> f16 for every non-NaN pattern: widen, narrow with RNE (torch
+    converts through float32 too; f16 overflow goes to infinity)."""
+    import torch
+    b = _all16(O.BF16)
+    want = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(torch.float16).view(torch.int16)
+    assert np.array_equal(O.cast_pair(b, O.BF16, O.F16), want.numpy().view(np.uint16))
+    h = _all16(O.F16)
+    want = torch.from_numpy(h.view(np.int16)).view(torch.float16).to(torch.bfloat16).view(torch.int16)
+    assert np.array_equal(O.cast_pair(h, O.F16, O.BF16), want.numpy().view(np.uint16))
+
+
+def test_cast_pair_fp8_sides():
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    finite = ~np.isnan(O.to_f32(codes, O.F8E4M3))
+    for dst in (O.BF16, O.F16):          # every finite e4m3 value is exact in bf16 / f16
+        got = O.cast_pair(codes, O.F8E4M3, dst)
+        assert np.array_equal(O.to_f32(got, dst)[finite], O.to_f32(codes, O.F8E4M3)[finite])
+    b = _all16(O.BF16)
+    x = O.to_f32(b, O.BF16)
+    inr = np.abs(x) <= 448
+    ref = torch.from_numpy(x[inr]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = O.cast_pair(b, O.BF16, O.F8E4M3)
+    assert np.array_equal(got[inr], ref)
+    assert np.all(got[~inr & np.isfinite(x)] & 0x7F == 0x7E)    # saturating (convert/fp8_f32.go:20-23)
+
+
+def test_cast_pair_f64_rounds_through_float32():
+    """shape_cast_intrinsic.go:83-114: float32(v) first, then the narrowing.  1 +
+    2^-8 + 2^-30 rounds to 1 + 2^-8 in f32, an exact bf16 tie that goes to even
+    (1.0); rounded straight from f64 it would be 1 + 2^-7."""
+    x = np.array([1 + 2**-8 + 2**-30], np.float64)
+    assert O.cast_pair(x, O.F64, O.BF16)[0] == 0x3F80
+    rng = np.random.default_rng(5)
+    v = np.concatenate([rng.standard_normal(1 << 16) * 100, rng.standard_normal(1000) * 1e-39,
+                        [np.inf, -np.inf, 0.0, -0.0, 1e300, -1e300, 5e-324]])
+    for dst in (O.BF16, O.F16, O.F8E4M3, O.F8E5M2):
+        with np.errstate(over="ignore"):
+            assert np.array_equal(O.cast_pair(v, O.F64, dst), O.from_f32(v.astype(np.float32), dst))
+    for src in (O.BF16, O.F16):
+        b = _all16(src)
+        assert np.array_equal(O.cast_pair(b, src, O.F64), O.to_f32(b, src).astype(np.float64))
