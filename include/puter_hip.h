@@ -368,6 +368,18 @@ PUTER_API int puter_hip_quant(void *dst, const void *src, int64_t count, float s
 PUTER_API int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,
                      int64_t inner, int64_t cols, int dtype, void *stream);
 
+/* Allocation-free Matmul.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same contract, formats and
+ * kernels as puter_hip_matmul, but the split-K partials go to a fixed 16 MiB
+ * device array per GPU (held until the process ends) instead of the growable
+ * scratch, so the call never allocates or frees.  That array is the most any
+ * split-K launch needs; a larger need would be PUTER_ERR_INVALID.  Every call on
+ * one GPU shares the array: calls that overlap on one GPU race, so issue them on
+ * one stream (or order them).  Calls on different GPUs are independent. */
+PUTER_API int puter_hip_matmul_noalloc(void *out, const void *left, const void *right, int64_t rows,
+                                       int64_t inner, int64_t cols, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -413,3 +413,9 @@ class Backend:
     def Matmul(self, out, left, right, rows, inner, cols, format):
         check(self.lib.puter_hip_matmul(_ptr(out), _ptr(left), _ptr(right), rows, inner, cols,
                                         format, self.stream()))
+
+    def MatmulNoAlloc(self, out, left, right, rows, inner, cols, format):
+        """Extension (no reference method): Matmul that never allocates (its split-K
+        partials use a fixed per-GPU device array); calls on one GPU must not overlap."""
+        check(self.lib.puter_hip_matmul_noalloc(_ptr(out), _ptr(left), _ptr(right), rows, inner, cols,
+                                                format, self.stream()))

@@ -592,9 +592,49 @@ int ScratchLease::finish() {
 }
 
 // Returns 1 when the shape does not fit the skinny kernel.
+// ---- the allocation-free Matmul (puter_hip_matmul_noalloc) -----------------
+// Its split-K partials live in a file-scope device array (one copy per GPU,
+// held until the process ends) instead of the growable scratch.  The array
+// holds 16 MiB, the most any split-K launch here can need: at most 512 blocks
+// (chunks x tiles) of 64 x 128 f32 partials for the 16-bit formats, of 64 x 64
+// for f32.  Host code never passes the array's name to a kernel (in host code it
+// is a stand-in, not a device address): it passes the address
+// hipGetSymbolAddress returns, looked up once per device on that device's first
+// call.  Every no-alloc call on a GPU shares that GPU's array, so such calls
+// must not overlap on one GPU; each call writes every partial it reads, so
+// nothing needs clearing between calls.
+namespace noalloc {
+constexpr size_t kScratchBytes = (size_t)512 * 64 * 128 * sizeof(float);
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+static std::mutex mu;
+static float *ptr[64];  // per device: scratch's device address
+
+static int address(float **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return fail(PUTER_ERR_UNAVAILABLE, "matmul (no-alloc): no device");
+    std::lock_guard<std::mutex> g(mu);
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(PUTER_ERR_UNAVAILABLE, "matmul (no-alloc): scratch address: %s", hipGetErrorString(e));
+        ptr[dev] = static_cast<float *>(p);
+    }
+    *out = ptr[dev];
+    return PUTER_OK;
+}
+}  // namespace noalloc
+
+// Where a call's split-K partials go: `fixed` (the no-alloc scratch) when set,
+// else a lease of the library's growable scratch.
+struct PartialsTarget {
+    float *fixed = nullptr;
+};
+
 template <int DT>
 static int launch_skinny(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
-                         hipStream_t s) {
+                         hipStream_t s, PartialsTarget tgt) {
     if (64 * K * 2 >= mm::OOB || sk::BK * N * 2 >= mm::OOB || N > 0x3FFFFFFF) return 1;
     const int64_t tiles_n = (N + sk::BN - 1) / sk::BN, tiles_m = (M + sk::BM - 1) / sk::BM;
     if (tiles_n > 0x7FFFFFFF) return 1;
@@ -612,11 +652,22 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
         matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
         return check_launch("matmul skinny");
     }
-    ScratchLease lease((size_t)(chunks * M * N) * sizeof(float), s);
+    const size_t need = (size_t)(chunks * M * N) * sizeof(float);
+    const int64_t quads = M * N / 4;
+    if (tgt.fixed) {
+        if (need > noalloc::kScratchBytes)
+            return fail(PUTER_ERR_INVALID, "matmul (no-alloc): split-K partials of %zu bytes exceed the %zu-byte scratch",
+                        need, noalloc::kScratchBytes);
+        p.ws = tgt.fixed;
+        matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
+        matmul_splitk_reduce_kernel<DT><<<(unsigned)std::min<int64_t>((quads + 255) / 256, 4096), 256, 0, s>>>(
+            static_cast<uint16_t *>(out), p.ws, quads, (int)chunks);
+        return check_launch("matmul split-k");
+    }
+    ScratchLease lease(need, s);
     if (lease.status()) return lease.status();
     p.ws = static_cast<float *>(lease.ptr());
     matmul_skinny_kernel<DT><<<grid, 256, 0, s>>>(p);
-    const int64_t quads = M * N / 4;
     matmul_splitk_reduce_kernel<DT><<<(unsigned)std::min<int64_t>((quads + 255) / 256, 4096), 256, 0, s>>>(
         static_cast<uint16_t *>(out), p.ws, quads, (int)chunks);
     const int rc = check_launch("matmul split-k");
@@ -626,10 +677,10 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
 
 template <int DT>
 static int launch_matmul16(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
-                           hipStream_t s) {
+                           hipStream_t s, PartialsTarget tgt) {
     if (N % 8 == 0 && K % 8 == 0 && aligned16(out) && aligned16(left) && aligned16(right)) {
         if (M <= 512) {
-            const int rc = launch_skinny<DT>(out, left, right, M, K, N, s);
+            const int rc = launch_skinny<DT>(out, left, right, M, K, N, s, tgt);
             if (rc != 1) return rc;
         }
         // 256 x 256 tiles (one 8-wave block per CU) from 160 such tiles up; below that
@@ -661,7 +712,7 @@ __global__ __launch_bounds__(256) void matmul_splitk_reduce_f32_kernel(float *c,
 // f32: 64 x 64 tiles; grids of fewer than 256 tiles split K (16-deep steps) into as
 // many chunks as keep the grid within 512 blocks, partials in the split-K scratch.
 static int launch_matmul_f32(float *out, const float *left, const float *right, int64_t M, int64_t K, int64_t N,
-                             hipStream_t s) {
+                             hipStream_t s, PartialsTarget tgt) {
     const dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
     if (grid.y > 65535) return fail(PUTER_ERR_INVALID, "matmul: too many rows");
     const int64_t tiles = (int64_t)grid.x * grid.y, steps = (K + kDepth - 1) / kDepth;
@@ -672,20 +723,29 @@ static int launch_matmul_f32(float *out, const float *left, const float *right, 
         matmul_f32_kernel<<<grid, 256, 0, s>>>(out, left, right, M, K, N, nullptr, K);
         return check_launch("matmul");
     }
-    ScratchLease lease((size_t)(chunks * M * N) * sizeof(float), s);
+    const size_t need = (size_t)(chunks * M * N) * sizeof(float);
+    auto launch = [&](float *ws) {
+        matmul_f32_kernel<<<dim3(grid.x, grid.y, (unsigned)chunks), 256, 0, s>>>(out, left, right, M, K, N, ws,
+                                                                                   per * kDepth);
+        matmul_splitk_reduce_f32_kernel<<<(unsigned)std::min<int64_t>((M * N + 255) / 256, 4096), 256, 0, s>>>(
+            out, ws, M * N, (int)chunks);
+        return check_launch("matmul split-k");
+    };
+    if (tgt.fixed) {
+        if (need > noalloc::kScratchBytes)
+            return fail(PUTER_ERR_INVALID, "matmul (no-alloc): split-K partials of %zu bytes exceed the %zu-byte scratch",
+                        need, noalloc::kScratchBytes);
+        return launch(tgt.fixed);
+    }
+    ScratchLease lease(need, s);
     if (lease.status()) return lease.status();
-    float *ws = static_cast<float *>(lease.ptr());
-    matmul_f32_kernel<<<dim3(grid.x, grid.y, (unsigned)chunks), 256, 0, s>>>(out, left, right, M, K, N, ws,
-                                                                               per * kDepth);
-    matmul_splitk_reduce_f32_kernel<<<(unsigned)std::min<int64_t>((M * N + 255) / 256, 4096), 256, 0, s>>>(
-        out, ws, M * N, (int)chunks);
-    const int rc = check_launch("matmul split-k");
+    const int rc = launch(static_cast<float *>(lease.ptr()));
     const int fin = lease.finish();
     return rc ? rc : fin;
 }
 
-extern "C" int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,
-                                int64_t inner, int64_t cols, int dtype, void *stream) {
+static int matmul_entry(void *out, const void *left, const void *right, int64_t rows, int64_t inner,
+                        int64_t cols, int dtype, void *stream, bool no_alloc) {
     if (rows < 0 || inner < 0 || cols < 0) return fail(PUTER_ERR_INVALID, "matmul: negative shape");
     if (dtype != PUTER_F32 && dtype != PUTER_F64 && dtype != PUTER_BF16 && dtype != PUTER_F16)
         return fail(PUTER_ERR_INVALID, "matmul: unsupported dtype %d", dtype);
@@ -698,14 +758,29 @@ extern "C" int puter_hip_matmul(void *out, const void *left, const void *right, 
         matmul_zero_kernel<<<generic_blocks(halves), 256, 0, s>>>(static_cast<uint16_t *>(out), halves);
         return check_launch("matmul");
     }
+    PartialsTarget tgt;
+    if (no_alloc) {
+        const int rc = noalloc::address(&tgt.fixed);
+        if (rc) return rc;
+    }
     switch (dtype) {
-    case PUTER_BF16: return launch_matmul16<PUTER_BF16>(out, left, right, rows, inner, cols, s);
-    case PUTER_F16: return launch_matmul16<PUTER_F16>(out, left, right, rows, inner, cols, s);
+    case PUTER_BF16: return launch_matmul16<PUTER_BF16>(out, left, right, rows, inner, cols, s, tgt);
+    case PUTER_F16: return launch_matmul16<PUTER_F16>(out, left, right, rows, inner, cols, s, tgt);
     case PUTER_F64:
         matmul_generic_kernel<PUTER_F64><<<generic_blocks(rows * cols), 256, 0, s>>>(out, left, right, rows, inner, cols);
         return check_launch("matmul");
     default: break;
     }
     return launch_matmul_f32(static_cast<float *>(out), static_cast<const float *>(left),
-                             static_cast<const float *>(right), rows, inner, cols, s);
+                             static_cast<const float *>(right), rows, inner, cols, s, tgt);
+}
+
+extern "C" int puter_hip_matmul(void *out, const void *left, const void *right, int64_t rows,
+                                int64_t inner, int64_t cols, int dtype, void *stream) {
+    return matmul_entry(out, left, right, rows, inner, cols, dtype, stream, false);
+}
+
+extern "C" int puter_hip_matmul_noalloc(void *out, const void *left, const void *right, int64_t rows,
+                                        int64_t inner, int64_t cols, int dtype, void *stream) {
+    return matmul_entry(out, left, right, rows, inner, cols, dtype, stream, true);
 }
