@@ -6,7 +6,7 @@ device.Backend method names for the norm / RoPE / gated activation / cast /
 paged-KV / attention / matmul / quantisation path.
 """
 from .backend import (  # noqa: F401
-    Backend, PuterError, RMSNormConfig, ModulatedLayerNormConfig, RoPEConfig,
+    Backend, DeviceBuffer, PuterError, RMSNormConfig, ModulatedLayerNormConfig, RoPEConfig,
     MultiAxisRoPEConfig, MultiHeadAttentionConfig, FlashAttentionConfig, DequantInt8Config, DequantInt4Config,
     F32, F16, BF16, F8E4M3, F8E5M2, I32, I8, I4, F64,
     RoPEModeInterleaved, RoPEModeHalf, RoPEScalingNone, RoPEScalingLlama3, dtype_of,

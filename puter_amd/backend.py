@@ -105,6 +105,25 @@ def _ptr(x):
     return x.data_ptr()
 
 
+class DeviceBuffer:
+    """A device allocation, or a view of one: the memory backend's device tensor
+    (reference: device/metal/workspace_darwin.go:18-77, the backend that
+    implements workspace slots).  A view shares its slot's device address with its
+    own shape, element format and byte count, and owns nothing."""
+
+    def __init__(self, lib, ptr, shape, element_format, byte_count, owns):
+        self._lib, self.ptr, self.shape = lib, ptr, tuple(shape)
+        self.element_format, self.byte_count, self.owns = element_format, byte_count, owns
+
+    def data_ptr(self):
+        return self.ptr
+
+    def Close(self):
+        if self.owns and self.ptr:
+            check(self._lib.puter_hip_free(C.c_void_p(self.ptr)))
+        self.ptr = 0
+
+
 class Backend:
     """The MI355X device backend (device.Backend subset on the hot path)."""
 
@@ -121,6 +140,38 @@ class Backend:
             import torch
             self._status = torch.zeros(1, dtype=torch.int32, device="cuda")
         return self._status
+
+    # ---- workspace slots: execution/workspace_resident.go:12-20 ----
+    def AllocateWorkspaceSlot(self, byteCount):
+        """One device allocation of byteCount bytes (shape [byteCount], Int8), which
+        NewResidentWorkspace carves into planned views; it stays on the device
+        until Close.  byteCount <= 0 is tensor.ErrShapeInvalid."""
+        if byteCount <= 0:
+            raise PuterError(_lib.ERR_INVALID, "tensor: invalid shape")
+        p = C.c_void_p()
+        check(self.lib.puter_hip_malloc(C.byref(p), byteCount))
+        return DeviceBuffer(self.lib, p.value, [byteCount], I8, byteCount, True)
+
+    def ViewWorkspaceSlot(self, slot, shape, elementFormat, byteCount):
+        """A view of a slot with another shape / element format: the same device
+        address, no copy.  byteCount outside [0, slot bytes] is
+        tensor.ErrShapeMismatch."""
+        if byteCount < 0 or byteCount > slot.byte_count:
+            raise PuterError(_lib.ERR_INVALID, "tensor: shape mismatch")
+        return DeviceBuffer(self.lib, slot.ptr, shape, elementFormat, byteCount, False)
+
+    def Upload(self, dst, data):
+        """Host bytes (a numpy array) into device memory on the backend's stream."""
+        check(self.lib.puter_hip_memcpy_htod(_ptr(dst), data.ctypes.data_as(C.c_void_p), data.nbytes,
+                                             self.stream()))
+        check(self.lib.puter_hip_stream_synchronize(self.stream()))
+
+    def Download(self, src, out):
+        """Device memory into a host numpy array (synchronises the stream)."""
+        check(self.lib.puter_hip_memcpy_dtoh(out.ctypes.data_as(C.c_void_p), _ptr(src), out.nbytes,
+                                             self.stream()))
+        check(self.lib.puter_hip_stream_synchronize(self.stream()))
+        return out
 
     def CheckStatus(self):
         """Synchronise, read and clear the status word; raise PuterError with the
