@@ -133,11 +133,53 @@ def norm_sweep(torch, be, puter, steps, warmup):
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "norm_wave_kernel<bf16,RMS,GR,16> (fused gated residual + RMSNorm)",
+            "kernel": "norm_row_kernel<bf16,RMS,GR,1> (fused gated residual + RMSNorm, a 1024-thread block per row)",
             "workload": f"{rmax}x{hmax} bf16, {dom_bytes} B/launch", "avg_launch_us": round(dom_ms * 1e3, 2)}
     del pool, r2, b2, h2
     torch.cuda.empty_cache()
     return ms, step_bytes, per, roof
+
+
+def norm_legs(torch, be, puter):
+    """The unfused legs of configs[1] at 65536 x 8192 bf16 (RMSNorm and LayerNorm
+    alone: read x, write y, 4 B/elem; GatedResidual alone: read residual and
+    branch, write hidden, 6 B/elem) and the 2-read/2-write stream ceiling of the
+    fused op on the same device (puter_hip_stream_probe, 16 B/vector x 4
+    streams over 1 GiB each), beside a 1 GiB device copy."""
+    import ctypes as C
+    rows, h = 65536, 8192
+    n = rows * h
+    bf = torch.bfloat16
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
+    x = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+    br = torch.randn(n, device="cuda", dtype=bf, generator=gen)
+    y = torch.empty_like(x)
+    mod = torch.randn(3 * h, device="cuda", dtype=bf, generator=gen)
+    gamma = (1 + 0.02 * torch.randn(h, device="cuda", generator=gen)).to(bf)
+    beta = (0.02 * torch.randn(h, device="cuda", generator=gen)).to(bf)
+    timer = Timer(torch)
+    res = {}
+    t = timer.time(lambda: be.RMSNorm(puter.RMSNormConfig(1e-5), x, gamma, y, rows, h, puter.BF16), 20, warmup=3)
+    res["rmsnorm_65536x8192_GBs"] = round(4 * n / (t * 1e-3) / 1e9, 1)
+    t = timer.time(lambda: be.LayerNorm(x, gamma, beta, y, rows, h, puter.BF16), 20, warmup=3)
+    res["layernorm_65536x8192_GBs"] = round(4 * n / (t * 1e-3) / 1e9, 1)
+    t = timer.time(lambda: be.GatedResidual(x, br, mod, y, rows, h, rows, 3 * h, 0, puter.BF16), 20, warmup=3)
+    res["gated_residual_65536x8192_GBs"] = round(6 * n / (t * 1e-3) / 1e9, 1)
+    # stream ceiling: four 1 GiB streams (x, br reused as a, b; y and a fourth as c, d)
+    d = torch.empty_like(x)
+    vectors = 2 * n // 16
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    for shape, name in ((0, "flat"), (1, "block_row"), (2, "wave_row")):
+        def probe(shape=shape):
+            rc = be.lib.puter_hip_stream_probe(C.c_void_p(x.data_ptr()), C.c_void_p(br.data_ptr()),
+                                               C.c_void_p(y.data_ptr()), C.c_void_p(d.data_ptr()), vectors, shape,
+                                               C.c_void_p(st()))
+            assert rc == 0, rc
+        t = timer.time(probe, 20, warmup=3)
+        res[f"stream_2r2w_{name}_GBs"] = round(4 * 16 * vectors / (t * 1e-3) / 1e9, 1)
+    del x, br, y, d
+    torch.cuda.empty_cache()
+    return res
 
 
 def rope_swiglu_casts(torch, be, puter):
@@ -636,7 +678,7 @@ def measure_traffic():
             for row in csv.DictReader(open(files[0])):
                 if row.get("Counter_Name") != counter:
                     continue
-                if "norm_wave_kernel" in row["Kernel_Name"]:
+                if "norm_wave_kernel" in row["Kernel_Name"] or "norm_row_kernel" in row["Kernel_Name"]:
                     kern.append(float(row["Counter_Value"]))
                 elif "copyBuffer" in row["Kernel_Name"]:
                     copy.append(float(row["Counter_Value"]))
@@ -693,6 +735,9 @@ def main():
     configs["copy_1GiB_GBs"] = round(2 * (1 << 30) / (t * 1e-3) / 1e9, 1)
     del src, dst
     torch.cuda.empty_cache()
+    configs.update(norm_legs(torch, be, puter))
+    log(f"norm legs: rms {configs['rmsnorm_65536x8192_GBs']} ln {configs['layernorm_65536x8192_GBs']} "
+        f"stream {configs['stream_2r2w_flat_GBs']} GB/s")
     if "rope" in only:
         configs.update(rope_swiglu_casts(torch, be, puter))
         log(f"rope/swiglu/casts: {configs}")

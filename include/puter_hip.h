@@ -380,6 +380,19 @@ PUTER_API int puter_hip_matmul(void *out, const void *left, const void *right, i
 PUTER_API int puter_hip_matmul_noalloc(void *out, const void *left, const void *right, int64_t rows,
                                        int64_t inner, int64_t cols, int dtype, void *stream);
 
+/* ------------------------------------------------------------------------ */
+/* Diagnostic (no counterpart in the reference): HBM stream probe with the   */
+/* fused GatedResidual+norm's traffic (read a and b, write c and d; vectors  */
+/* of 16 bytes each) and no arithmetic, so its rate is the norm kernels'     */
+/* practical ceiling on the same device.  shape 0: one vector of each input  */
+/* per thread; 1: a 1024-thread block per 1024-vector row with a block-wide  */
+/* sum between the stores; 2: a wave per 1024-vector row, 16 vectors per     */
+/* lane.  Shapes 1 and 2 need vectors % 1024 == 0; all buffers 16-byte       */
+/* aligned.                                                                  */
+/* ------------------------------------------------------------------------ */
+PUTER_API int puter_hip_stream_probe(const void *a, const void *b, void *c, void *d, int64_t vectors,
+                                     int shape, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,7 +18,7 @@ LIBRARY = os.path.join(HERE, "libputer_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["runtime.hip", "cast.hip", "norm.hip", "rope.hip", "gated.hip", "page.hip",
-           "attention.hip", "prefill.hip", "decode.hip", "flash.hip", "matmul.hip", "quant.hip"]
+           "attention.hip", "prefill.hip", "decode.hip", "flash.hip", "matmul.hip", "quant.hip", "probe.hip"]
 
 HIPFLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

@@ -8,11 +8,13 @@
 // row differs (lane-sequential then a wave64 butterfly), which the reference's
 // own SIMD kernels also change.
 //
-// Fast path: one wave64 per row, 4 rows per 256-thread block.  The row lives in
-// registers as VPL 16-byte vectors per lane (lane l owns vectors j*64 + l, so
-// each wave-wide load is one contiguous 1 KiB burst), so every tensor is read
-// once and written once: for the fused op, 8 B/elem of HBM traffic in bf16.
-// Reductions are register-only wave butterflies (no LDS, no barriers).
+// Fast paths keep the row in registers, so every tensor is read once and
+// written once (for the fused op, 8 B/elem of HBM traffic in bf16):
+//   - norm_row_kernel: a block per row, one 16-byte vector per thread per
+//     tensor (long rows, many rows);
+//   - norm_wave_kernel: one wave64 per row, 4 rows per 256-thread block, the row
+//     as VPL 16-byte vectors per lane (lane l owns vectors j*64 + l, so each
+//     wave-wide load is one contiguous 1 KiB burst); register-only butterflies.
 // Any other shape or alignment uses the generic block-per-row kernel, which
 // re-reads the row from memory for each pass.
 #include "common.hpp"
@@ -224,6 +226,125 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     }
 }
 
+// ------------------------------------------------------- row-block path --
+// One block per row, the row spread over the whole block: thread t owns the V
+// 16-byte vectors j*T + t (T = blockDim.x, T*V*N = H), so every tensor is still
+// read once and written once, but each thread keeps only V (1 for bf16 rows of
+// up to 8192) loads of each input in flight.  Measured on MI355X, this launch
+// shape (many threads, one vector each) sustains ~10% more HBM bandwidth on the
+// 2-read / 2-write stream than a wave per row holding the row in 4-16 vectors
+// per lane.  The sums go through a wave butterfly and one LDS round (T/64
+// partials, one barrier per reduction).
+template <int DT, int OP, bool GR, int V>
+__global__ __launch_bounds__(1024) void norm_row_kernel(NormArgs a) {
+#pragma clang fp contract(off)
+    constexpr int N = Vec<DT>::N;
+    __shared__ float red[2][16];
+    const int T = blockDim.x, t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = T >> 6;
+    const int64_t row = blockIdx.x;
+    const int64_t H = a.H;
+    const size_t row_vec = (size_t)row * (size_t)(H / N);
+    const int64_t batch = row / a.rows_per_batch;
+    auto block_total = [&](float v, int slot) __attribute__((always_inline)) {
+        v = wave_sum(v);
+        if (lane == 0) red[slot][wave] = v;
+        __syncthreads();
+        float s = 0.0f;
+        for (int w = 0; w < nw; ++w) s += red[slot][w];
+        return s;
+    };
+
+    uint4 hv[V];
+    if constexpr (GR) {
+        const uint4 *res = reinterpret_cast<const uint4 *>(a.x) + row_vec;
+        const uint4 *br = reinterpret_cast<const uint4 *>(a.branch) + row_vec;
+        const uint4 *gate = reinterpret_cast<const uint4 *>(a.mod) + (size_t)(batch * a.mod_cols + a.gate_off) / N;
+        uint4 rv[V], bv[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            rv[j] = ld_stream(res + j * T + t);
+            bv[j] = ld_stream(br + j * T + t);
+        }
+        uint4 *hid = reinterpret_cast<uint4 *>(a.hidden) + row_vec;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            float r[N], b[N], g[N], o[N];
+            unpack_vec<DT>(rv[j], r);
+            unpack_vec<DT>(bv[j], b);
+            unpack_vec<DT>(gate[j * T + t], g);
+#pragma unroll
+            for (int i = 0; i < N; ++i) o[i] = r[i] + g[i] * b[i];
+            hv[j] = pack_vec<DT>(o);
+            st_stream(hv[j], hid + j * T + t);
+        }
+    } else {
+        const uint4 *x = reinterpret_cast<const uint4 *>(a.x) + row_vec;
+#pragma unroll
+        for (int j = 0; j < V; ++j) hv[j] = ld_stream(x + j * T + t);
+    }
+
+    float mean = 0.0f, inv;
+    if constexpr (OP == OP_RMS || OP == OP_ADAPTIVE) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            float h[N];
+            unpack_vec<DT>(hv[j], h);
+#pragma unroll
+            for (int i = 0; i < N; ++i) ss += h[i] * h[i];
+        }
+        inv = rms_inverse<DT, OP>(block_total(ss, 0), H, a.eps);
+    } else {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            float h[N];
+            unpack_vec<DT>(hv[j], h);
+#pragma unroll
+            for (int i = 0; i < N; ++i) s += h[i];
+        }
+        mean = ln_mean<DT, OP>(block_total(s, 0), H);
+        float sq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            float h[N];
+            unpack_vec<DT>(hv[j], h);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const float d = h[i] - mean;
+                sq += d * d;
+            }
+        }
+        inv = ln_inverse<DT, OP>(block_total(sq, 1), H, a.eps);
+    }
+
+    const uint4 *gp;
+    const uint4 *bp = nullptr;
+    if constexpr (OP == OP_RMS || OP == OP_LN) {
+        gp = reinterpret_cast<const uint4 *>(a.scale);
+        if constexpr (OP == OP_LN) bp = reinterpret_cast<const uint4 *>(a.bias);
+    } else {
+        const uint4 *m = reinterpret_cast<const uint4 *>(a.mod) + (size_t)(batch * a.mod_cols + a.mod_off) / N;
+        if constexpr (OP == OP_ADAPTIVE) { gp = m; bp = m + H / N; }      // scale, shift
+        else { bp = m; gp = m + H / N; }                                  // shift, scale
+    }
+    uint4 *out = reinterpret_cast<uint4 *>(a.out) + row_vec;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        float h[N], g[N], b[N], o[N];
+        unpack_vec<DT>(hv[j], h);
+        unpack_vec<DT>(gp[j * T + t], g);
+        if (bp) unpack_vec<DT>(bp[j * T + t], b);
+        else {
+#pragma unroll
+            for (int i = 0; i < N; ++i) b[i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) o[i] = apply_one<DT, OP>(h[i], mean, inv, g[i], b[i]);
+        st_stream(pack_vec<DT>(o), out + j * T + t);
+    }
+}
+
 // ---------------------------------------------------------- generic path --
 __device__ __forceinline__ float block_sum(float v, float *smem) {
     v = wave_sum(v);
@@ -296,31 +417,55 @@ __global__ __launch_bounds__(256) void norm_block_kernel(NormArgs a, int has_nor
     }
 }
 
-// Element-wise gated residual alone, 16-byte vectors, flat over rows*H.
+// Element-wise gated residual alone, 16-byte vectors: block (row, 256-vector
+// chunk of the row), one vector of each input per thread, so no index division
+// and the launch shape that streams HBM best (one vector per thread).
 template <int DT>
 __global__ __launch_bounds__(256) void gated_residual_vec_kernel(NormArgs a) {
 #pragma clang fp contract(off)
     constexpr int N = Vec<DT>::N;
     const int64_t vec_per_row = a.H / N;
-    const int64_t total = a.rows * vec_per_row;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < total; v += stride) {
-        const int64_t row = v / vec_per_row, col = v - row * vec_per_row;
-        const int64_t batch = row / a.rows_per_batch;
-        float r[N], b[N], g[N], o[N];
-        load_vec<DT>(a.x, (size_t)v, r);
-        load_vec<DT>(a.branch, (size_t)v, b);
-        load_vec<DT>(a.mod, (size_t)((batch * a.mod_cols + a.gate_off) / N + col), g);
+    const int64_t col = (int64_t)blockIdx.y * 256 + threadIdx.x;
+    if (col >= vec_per_row) return;
+    const int64_t row = blockIdx.x;
+    const int64_t batch = row / a.rows_per_batch;
+    const size_t v = (size_t)row * (size_t)vec_per_row + (size_t)col;
+    float r[N], b[N], g[N], o[N];
+    unpack_vec<DT>(ld_stream(reinterpret_cast<const uint4 *>(a.x) + v), r);
+    unpack_vec<DT>(ld_stream(reinterpret_cast<const uint4 *>(a.branch) + v), b);
+    load_vec<DT>(a.mod, (size_t)((batch * a.mod_cols + a.gate_off) / N + col), g);
 #pragma unroll
-        for (int i = 0; i < N; ++i) o[i] = r[i] + g[i] * b[i];
-        reinterpret_cast<uint4 *>(a.hidden)[v] = pack_vec<DT>(o);
-    }
+    for (int i = 0; i < N; ++i) o[i] = r[i] + g[i] * b[i];
+    st_stream(pack_vec<DT>(o), reinterpret_cast<uint4 *>(a.hidden) + v);
 }
 
 // --------------------------------------------------------------- launch --
 template <int DT, int OP, bool GR>
 static int launch_norm(const NormArgs &a, hipStream_t s, bool vec_ok) {
     constexpr int N = Vec<DT>::N;
+    // Launch shape, chosen by same-process measurements on MI355X (bf16 sweep of
+    // 1024 / 16384 / 65536 rows x 2048 / 4096 / 8192): with thousands of rows and
+    // rows of at least 512 16-byte vectors, a block per row (one vector per
+    // thread per tensor) streams 3-12% faster than a wave per row; the fused
+    // GatedResidual+RMSNorm does best at up to 1024 threads per row, norms with
+    // two reductions (LayerNorm, modulated) and the unfused norms at 512.  Fewer
+    // rows (latency-bound) and shorter rows keep the wave per row.
+    const int64_t U = a.H / N;
+    constexpr bool two_pass = OP == OP_LN || OP == OP_MODULATED;
+    if (vec_ok && a.H % (64 * N) == 0 && a.rows >= 4096 && U >= 512) {
+        const int64_t max_t = (GR && !two_pass) ? 1024 : 512;
+        int V = 1;
+        while (U / V > max_t) V *= 2;
+        if (V <= 4 && U % V == 0 && (U / V) % 64 == 0) {
+            const unsigned T = (unsigned)(U / V), blocks = (unsigned)a.rows;
+            switch (V) {
+            case 1: norm_row_kernel<DT, OP, GR, 1><<<blocks, T, 0, s>>>(a); break;
+            case 2: norm_row_kernel<DT, OP, GR, 2><<<blocks, T, 0, s>>>(a); break;
+            default: norm_row_kernel<DT, OP, GR, 4><<<blocks, T, 0, s>>>(a); break;
+            }
+            return check_launch("norm");
+        }
+    }
     if (vec_ok && a.H % (64 * N) == 0) {
         const int64_t vpl = a.H / (64 * N);
         const unsigned blocks = (unsigned)((a.rows + 3) / 4);
@@ -458,14 +603,13 @@ int puter_hip_gated_residual(const void *residual, const void *branch, const voi
     const int n = 16 / dtype_bytes(dtype);
     const bool vec_ok = aligned16(residual) && aligned16(branch) && aligned16(modulation) &&
                         aligned16(output) && last_dim % n == 0 && modulation_cols % n == 0;
-    if (vec_ok) {
-        const int64_t total = rows * (last_dim / n);
-        int64_t blocks = (total + 255) / 256;
-        if (blocks > 16384) blocks = 16384;
+    const int64_t chunks = (last_dim / n + 255) / 256;
+    if (vec_ok && chunks <= 65535) {
+        const dim3 grid((unsigned)rows, (unsigned)chunks);
         switch (dtype) {
-        case PUTER_F32: gated_residual_vec_kernel<PUTER_F32><<<(unsigned)blocks, 256, 0, s>>>(a); break;
-        case PUTER_BF16: gated_residual_vec_kernel<PUTER_BF16><<<(unsigned)blocks, 256, 0, s>>>(a); break;
-        case PUTER_F16: gated_residual_vec_kernel<PUTER_F16><<<(unsigned)blocks, 256, 0, s>>>(a); break;
+        case PUTER_F32: gated_residual_vec_kernel<PUTER_F32><<<grid, 256, 0, s>>>(a); break;
+        case PUTER_BF16: gated_residual_vec_kernel<PUTER_BF16><<<grid, 256, 0, s>>>(a); break;
+        case PUTER_F16: gated_residual_vec_kernel<PUTER_F16><<<grid, 256, 0, s>>>(a); break;
         }
         return check_launch("gated residual");
     }

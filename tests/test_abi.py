@@ -89,6 +89,10 @@ def test_cast_activation_page_validation(lib):
     assert lib.puter_hip_kv_page_gather(FAKE, FAKE, FAKE, 4, 16, 8, 2, 0, 0, FAKE + 1, None) == _lib.ERR_INVALID
     assert lib.puter_hip_kv_page_write_fp8(FAKE, FAKE, FAKE, FAKE, 4, 16, 2, 128, 2, 0, FAKE, 2, FAKE + 2,
                                            None) == _lib.ERR_INVALID
+    # stream probe: shapes 0-2 only, rows of 1024 vectors for the row shapes
+    assert lib.puter_hip_stream_probe(FAKE, FAKE, FAKE, FAKE, 1024, 3, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_stream_probe(FAKE, FAKE, FAKE, FAKE, 1000, 1, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_stream_probe(None, None, None, None, 0, 0, None) == _lib.OK
     # RoPEPairs is F32 only (device/cpu/rope/ops.go:10-14); zero pairs is a no-op
     assert lib.puter_hip_rope_pairs(FAKE, FAKE, FAKE, FAKE, 8, 2, None) == _lib.ERR_INVALID
     assert lib.puter_hip_rope_pairs(None, None, None, None, 0, 0, None) == _lib.OK

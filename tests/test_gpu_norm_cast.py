@@ -168,3 +168,50 @@ def test_norm_errors_raise(backend):
         backend.LayerNorm(x, x, x, x, 4, 8, O.F8E4M3)  # unsupported dtype
     # zero-sized work is a no-op, as compute.go:19-21
     backend.LayerNorm(x, x, x, x, 0, 8, O.F32)
+
+
+# the block-per-row kernel (>= 4096 rows of >= 512 16-byte vectors): every norm
+# op and dtype, the fused ops included, against the oracle
+@pytest.mark.parametrize("dt,h", [(O.BF16, 4096), (O.BF16, 8192), (O.F16, 8192), (O.F32, 2048), (O.F32, 8192)])
+def test_norms_block_per_row(backend, dt, h):
+    import puter_amd
+    rows, rpb = 4096, 1024
+    x = encode(seeded(7100 + h + dt, (rows, h)), dt)
+    g = encode(seeded(7200 + h, (h,), 1.0, 0.02), dt)
+    b = encode(seeded(7300 + h, (h,), 0.0, 0.02), dt)
+    out = empty_dev((rows, h), NP[dt])
+    dx = to_dev(x)
+    backend.RMSNorm(puter_amd.RMSNormConfig(1e-5), dx, to_dev(g), out, rows, h, dt)
+    assert_close(decode(to_host(out, NP[dt]), dt), decode(O.rmsnorm(x, g, 1e-5, dt), dt), TOL[dt],
+                 REDUCE_ELEM_TOL[dt], what="rmsnorm")
+    backend.LayerNorm(dx, to_dev(g), to_dev(b), out, rows, h, dt)
+    assert_close(decode(to_host(out, NP[dt]), dt), decode(O.layernorm(x, g, b, dt), dt), TOL[dt],
+                 REDUCE_ELEM_TOL[dt], what="layernorm")
+    mod = encode(seeded(7400 + h, (rows // rpb, 6 * h), 0.0, 0.5), dt)
+    backend.AdaptiveRMSNorm(puter_amd.RMSNormConfig(1e-6), dx, to_dev(mod), out, rows, h, rpb, 6 * h, dt)
+    assert_close(decode(to_host(out, NP[dt]), dt), decode(O.adaptive_rmsnorm(x, mod, rpb, 1e-6, dt), dt),
+                 TOL[dt], REDUCE_ELEM_TOL[dt], what="adaptive")
+    backend.ModulatedLayerNorm(puter_amd.ModulatedLayerNormConfig(1e-6, 1), dx, to_dev(mod), out, rows, h, rpb,
+                               6 * h, dt)
+    assert_close(decode(to_host(out, NP[dt]), dt), decode(O.modulated_layernorm(x, mod, rpb, 1e-6, 1, dt), dt),
+                 TOL[dt], REDUCE_ELEM_TOL[dt], what="modulated")
+    br = encode(seeded(7500 + h, (rows, h)), dt)
+    gm = encode(seeded(7600 + h, (rows // rpb, 3 * h)), dt)
+    hid = empty_dev((rows, h), NP[dt])
+    hid_ref = O.gated_residual(x, br, gm, rpb, 0, dt)
+    for kind in ("rms", "ln"):
+        if kind == "rms":
+            backend.GatedResidualRMSNorm(puter_amd.RMSNormConfig(1e-5), dx, to_dev(br), to_dev(gm), to_dev(g), hid,
+                                         out, rows, h, rpb, 3 * h, 0, dt)
+            y_ref = O.rmsnorm(hid_ref, g, 1e-5, dt)
+        else:
+            backend.GatedResidualLayerNorm(dx, to_dev(br), to_dev(gm), to_dev(g), to_dev(b), hid, out, rows, h,
+                                           rpb, 3 * h, 0, dt)
+            y_ref = O.layernorm(hid_ref, g, b, dt)
+        got_h = to_host(hid, NP[dt])
+        if dt != O.F32:
+            assert np.array_equal(got_h, hid_ref), kind
+        else:
+            assert_close(got_h, hid_ref, TOL[dt], REDUCE_ELEM_TOL[dt], what="hidden")
+        assert_close(decode(to_host(out, NP[dt]), dt), decode(y_ref, dt), TOL[dt], REDUCE_ELEM_TOL[dt],
+                     what=f"fused {kind}")
