@@ -624,8 +624,10 @@ def profile_workload(torch, be, puter, spec, launches):
     """Counter-collection workloads, one kernel family per run (`--profile-workload
     NAME --profile-launches N`): `norm:ROWSxHIDDEN` (fused GatedResidual+RMSNorm
     bf16 on one shape, each launch on the next window of 1 GiB pools so none is
-    served from the 256 MB last-level cache), `prefill`, `decode_bf16` / `decode_fp8`
-    (configs[4]).  Each launch is preceded by nothing else on the stream."""
+    served from the 256 MB last-level cache, then one 1 GiB calibration copy),
+    `stream` (the 2-read/2-write stream probe in its three launch shapes),
+    `prefill` (configs[3]), `decode_bf16` / `decode_fp8` (configs[4]).  Each
+    launch is preceded by nothing else on the stream."""
     if spec.startswith("norm:"):
         r, h = (int(x) for x in spec[5:].split("x"))
         gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
@@ -636,6 +638,23 @@ def profile_workload(torch, be, puter, spec, launches):
         for _ in range(launches):
             res, br, hid, out = pool.next(r * h)
             be.GatedResidualRMSNorm(cfg, res, br, mod, gamma, hid, out, r, h, r, 3 * h, 0, puter.BF16)
+        # calibration for FETCH_SIZE / WRITE_SIZE: one 1 GiB device copy
+        src = pool.res[: (1 << 30) // 2]
+        pool.hid[: src.numel()].copy_(src)
+    elif spec == "stream":
+        # the 2-read/2-write stream ceiling: puter_hip_stream_probe over four 1 GiB
+        # buffers in its three launch shapes (flat grid, block per 16 KiB row,
+        # wave per 16 KiB row), `launches` times each
+        import ctypes as C
+        n = (1 << 30) // 2
+        bufs = [torch.empty(n, device="cuda", dtype=torch.bfloat16).fill_(1.0) for _ in range(4)]
+        vectors = 2 * n // 16
+        stream = torch.cuda.current_stream().cuda_stream
+        for shape in (0, 1, 2):
+            for _ in range(launches):
+                rc = be.lib.puter_hip_stream_probe(*(C.c_void_p(b.data_ptr()) for b in bufs), vectors, shape,
+                                                   C.c_void_p(stream))
+                assert rc == 0, rc
     elif spec == "prefill":
         fn = prefill(torch, be, puter, return_fn=True)
         for _ in range(launches):
@@ -703,7 +722,7 @@ def main():
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant kernel N times plus a 1 GiB calibration copy")
     ap.add_argument("--profile-workload", default="", metavar="NAME",
-                    help="only run one counter-collection workload: norm:RxH, prefill, decode_bf16, decode_fp8")
+                    help="only run one counter-collection workload: norm:RxH, stream, prefill, decode_bf16, decode_fp8")
     ap.add_argument("--profile-launches", type=int, default=5, metavar="N")
     ap.add_argument("--profile-matmul", type=int, default=0, metavar="N",
                     help="only run the bf16 Matmul 8192^3 N times (counter collection)")

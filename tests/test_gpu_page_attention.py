@@ -290,6 +290,32 @@ def test_mha_batched_prefill_bf16(backend):
         assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"batch {i}")
 
 
+def test_prefill_rows_agree_with_one_row_path_bf16(backend):
+    """The MFMA prefill keeps each bf16 score dot in f32, where the reference
+    (typed_compute.go:16-20, dot/bf16_generic.go:9-21) and the one-row kernel
+    round it to bf16.  Row i of a causal prefill sees keys 0..i, exactly what a
+    one-row call over the first i+1 keys sees: the two paths agree to the bf16
+    bar elementwise on every element above a tenth of the row's largest."""
+    import puter_amd
+    dt, s, h, kvh, d = O.BF16, 512, 8, 2, 128
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(41, (s, h * d), 0.0, 4 * std), dt)
+    k = encode(seeded(42, (s, kvh * d), 0.0, 4 * std), dt)
+    v = encode(seeded(43, (s, kvh * d)), dt)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, True, 0, 0.0, kvh)
+    out = empty_dev((s, h * d), np.uint16)
+    backend.MultiHeadAttention(cfg, to_dev(q), to_dev(k), to_dev(v), out, s, s, dt)
+    rows = decode(to_host(out, np.uint16), dt)
+    for i in (0, 63, 64, 300, s - 1):
+        one = empty_dev((1, h * d), np.uint16)
+        backend.MultiHeadAttention(cfg, to_dev(q[i:i + 1]), to_dev(k[:i + 1].copy()), to_dev(v[:i + 1].copy()),
+                                   one, 1, i + 1, dt)
+        ref1 = decode(to_host(one, np.uint16), dt)[0]
+        assert_close(rows[i], ref1, TOL[dt], elem_tol=2e-2, floor=0.1, what=f"row {i}")
+        oracle_row = decode(O.mha(q[i:i + 1], k[:i + 1], v[:i + 1], h, d, causal=True, kv_heads=kvh, dtype=dt), dt)
+        assert_close(ref1, oracle_row[0], TOL[dt], elem_tol=2e-2, floor=0.1, what=f"one-row {i} vs oracle")
+
+
 @pytest.mark.parametrize("b,sq,sk,h,kvh,causal", [
     (1, 1024, 1024, 8, 2, True),    # several diagonal and full tiles per block
     (2, 333, 333, 4, 1, True),      # ragged: partial query and key tiles

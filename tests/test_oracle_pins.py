@@ -328,6 +328,28 @@ def test_page_write_reference_kat_and_chain():
                      np.array([0, 0], np.int32), 2, 1, storage_offset=6, page_count=3)
 
 
+def test_page_write_duplicate_slots_keep_the_highest_row():
+    """page_generic.go:23-27 copies rows in order, so for every (page, slot) the
+    stored row is the highest row index that targets it; slots no row targets
+    keep the storage's bytes."""
+    rng = np.random.default_rng(11)
+    pages, ps, inner, rows = 3, 4, 5, 40          # 12 slots, 40 rows: many duplicates
+    ids = rng.integers(0, pages, rows).astype(np.int32)
+    offs = rng.integers(0, ps, rows).astype(np.int32)
+    vals = rng.standard_normal((rows, inner)).astype(np.float32)
+    st = rng.standard_normal(pages * ps * inner).astype(np.float32)
+    got = O.page_write(st, vals, ids, offs, ps, inner).reshape(pages, ps, inner)
+    winner = {}
+    for r in range(rows):
+        key = (int(ids[r]), int(offs[r]))
+        winner[key] = max(winner.get(key, -1), r)
+    base = st.reshape(pages, ps, inner)
+    for p in range(pages):
+        for s in range(ps):
+            want = vals[winner[(p, s)]] if (p, s) in winner else base[p, s]
+            assert np.array_equal(got[p, s], want), (p, s)
+
+
 def test_page_gather_identity_is_copy():
     st = seeded(4, (8 * 4 * 6,))
     assert np.array_equal(O.page_gather(st, np.arange(8, dtype=np.int32), 4, 6, 32).ravel(), st)
