@@ -23,12 +23,16 @@
 //     reach the operand layout through a wave-private LDS tile (swizzled, bank-
 //     conflict free), B = the G query heads of the kv group, zero-padded to 16
 //     columns; a lane then holds 8 scores of one head.
-//   values: O[head, d] += p[head, token] * V[token, d] on the VALU: lane owns 8
-//     dims of every 4th token, reads the token's G probabilities from a
-//     wave-private LDS row, and accumulates G x 8 sums.
-// The 4 token-group partials are summed in registers (lane-row swaps) into one
-// (m, l, o[D]) per query head and split; decode_combine_kernel merges the
-// splits by log-sum-exp.
+//   values (decode_block_kernel): O^T[d, head] = V^T . P^T on the same MFMA,
+//     V rows (fp8 widened to bf16) through the wave's LDS tile and read back
+//     transposed by ds_read_b64_tr_b16, P as bf16 hi + lo halves; the VALU FMA
+//     form it replaced left the fp8 kernel VALU-bound (78% VALU busy).
+//   values (decode_kernel): O[head, d] += p[head, token] * V[token, d] on the
+//     VALU: lane owns 8 dims of every 4th token, reads the token's G
+//     probabilities from a wave-private LDS row, accumulates G x 8 sums, and
+//     the 4 token-group partials are summed by lane-row swaps.
+// Each split leaves one (m, l, o[D]) per query head; decode_combine_kernel
+// merges the splits by log-sum-exp.
 #include "attention.hpp"
 #include "common.hpp"
 #include <algorithm>
@@ -42,6 +46,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 struct DecodeArgs {
     const uint16_t *q;
@@ -316,21 +322,21 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 
 // Paged decode, block form: one 256-thread block per (kv head, 256-token split,
 // sequence); wave w takes the split's tokens 64w .. 64w + 63 and issues every K
-// and V row load of its 64 tokens at once (32 KB of bf16 in flight per wave),
-// then computes them: scores on MFMA through a wave-private LDS tile, the
-// softmax of its 64 tokens against their own max, P.V on the VALU.  The four
-// waves' (m, l, o) merge through LDS into the split's partial, the same
-// partial the wave-per-split kernel writes.  Scores go 32 tokens at a time
-// through an 8 KB per-wave tile, so three blocks share a CU.  Measured against
-// the sub-chunk walk in one process on the configs[4] pool: bf16 +1%, fp8 +4%.
+// and V row load of its 64 tokens at once (16-byte pieces: 32 KB of bf16 in
+// flight per wave), then computes them: scores on MFMA through a wave-private
+// LDS tile, the softmax of its 64 tokens against their own max, P.V on MFMA
+// through the same tile.  The four waves' (m, l, o) merge through LDS into the
+// split's partial, the same partial the wave-per-split kernel writes.  Measured
+// in one process on the configs[4] pool against the sub-chunk walk: bf16 +1%,
+// fp8 +4%; MFMA P.V with 16-byte fp8 row pieces then took fp8 from 144.6 to
+// 138.0 us (bf16 unchanged).
 template <int KV, int G>
 __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     constexpr int D = 128, TW = 64;
     constexpr bool BF = KV == PUTER_BF16;
-    constexpr int RB = BF ? 256 : 128;            // KV row bytes (one kv head)
-    using VT = typename std::conditional<BF, uint4, uint2>::type;
-    __shared__ __attribute__((aligned(1024))) char k_lds[4][32 * RB];   // per-wave 32-row K tiles, then the o merge
-    __shared__ float p_lds[4][TW][G];
+    // per-wave 32-row tiles: K rows (256 bytes bf16, 128 fp8), then V rows widened
+    // to bf16 (256 bytes), then the o merge
+    __shared__ __attribute__((aligned(1024))) char k_lds[4][32 * 256];
     __shared__ float ml_lds[4][G][2];
 
     const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
@@ -346,11 +352,11 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     constexpr int EB = BF ? 2 : 1;
     const uint8_t *kpool = static_cast<const uint8_t *>(a.kp);
     const uint8_t *vpool = static_cast<const uint8_t *>(a.vp);
-    float acc[G][8];
+    float acc[8][4];   // lane (grp, l16 < G): O[head l16][16 mt + 4 grp + r] = acc[mt][r]
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
+        for (int r = 0; r < 4; ++r) acc[mt][r] = 0.0f;
     float m_w = -INFINITY, l_w = 0.0f;   // lane l16 < G: head l16's max (log2 domain) and sum
 
     if (tw0 < ctx) {   // wave-uniform
@@ -363,20 +369,18 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                 if (page >= 0 && page < a.num_pages) myrow = page * ps + (tok - pidx * ps);
             }
         }
-        // every K and V row of the wave's 64 tokens: lane group grp takes token
-        // 4k + grp, lane l16 its piece l16 (dead rows read pool row 0: masked below)
-        VT kb[16], vb[16];
+        // every K and V row of the wave's 64 tokens, 16 bytes per lane: bf16 rows
+        // (256 bytes) as token 4k + grp, piece l16; fp8 rows (128 bytes) as token
+        // 8k + g8, piece l8 (dead rows read pool row 0: masked below)
+        constexpr int NL = BF ? 16 : 8;   // row loads per lane and tensor
+        const int g8 = lane >> 3, l8 = lane & 7;
+        uint4 kb[NL], vb[NL];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int row = max(__shfl(myrow, 4 * k + grp, 64), 0);
-            const int64_t off = ((int64_t)row * inner + head_off) * EB + (int64_t)sizeof(VT) * l16;
-            if constexpr (BF) {
-                kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
-                vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
-            } else {
-                kb[k] = *reinterpret_cast<const uint2 *>(kpool + off);
-                vb[k] = *reinterpret_cast<const uint2 *>(vpool + off);
-            }
+        for (int k = 0; k < NL; ++k) {
+            const int row = max(__shfl(myrow, BF ? 4 * k + grp : 8 * k + g8, 64), 0);
+            const int64_t off = ((int64_t)row * inner + head_off) * EB + 16 * (BF ? l16 : l8);
+            kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
+            vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
         }
         // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero
         bf16x8_t qb[4];
@@ -390,17 +394,27 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
         const uint64_t live = __ballot(myrow >= 0);   // token t live iff bit t
         char *tile = k_lds[wave];
         // scores S^T[token, head], 32 tokens at a time: K rows -> the wave's LDS
-        // tile (row r = 4k + grp of the half, piece l16 at l16 ^ swizzle(r)), then
-        // A = tile rows 16i + l16, B = Q^T; lane: head l16, tokens 16i + 4grp + r
+        // tile, then A = tile rows 16i + l16, B = Q^T; lane: head l16, tokens
+        // 16i + 4grp + r.  bf16 rows keep 16-byte piece c at c ^ (r % 16); fp8 rows
+        // (128 bytes) keep it at c ^ ((r / 2) % 8), i.e. 8-byte unit u at
+        // u ^ 2 ((r / 2) % 8): the 16 rows an operand read touches then fall on
+        // distinct banks (rows r and r ^ 1 lie 128 bytes apart)
         f32x4_t s[4];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             if (half) __builtin_amdgcn_wave_barrier();   // the first half's tile reads are done
+            if constexpr (BF) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int r = 4 * k + grp;
-                if constexpr (BF) *reinterpret_cast<uint4 *>(tile + r * 256 + ((l16 ^ (r & 15)) << 4)) = kb[8 * half + k];
-                else *reinterpret_cast<uint2 *>(tile + r * 128 + ((l16 ^ ((r >> 1) & 7)) << 3)) = kb[8 * half + k];
+                for (int k = 0; k < 8; ++k) {
+                    const int r = 4 * k + grp;
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + ((l16 ^ (r & 15)) << 4)) = kb[8 * half + k];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int r = 8 * k + g8;
+                    *reinterpret_cast<uint4 *>(tile + r * 128 + ((l8 ^ ((r >> 1) & 7)) << 4)) = kb[4 * half + k];
+                }
             }
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -411,7 +425,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                 for (int t = 0; t < 4; ++t) {
                     uint4 kv;
                     if constexpr (BF) kv = *reinterpret_cast<const uint4 *>(tile + row * 256 + (((4 * t + grp) ^ l16) << 4));
-                    else kv = fp8x8_to_bf16(*reinterpret_cast<const uint2 *>(tile + row * 128 + (((4 * t + grp) ^ ((l16 >> 1) & 7)) << 3)));
+                    else kv = fp8x8_to_bf16(*reinterpret_cast<const uint2 *>(tile + row * 128 + (((4 * t + grp) ^ (2 * ((l16 >> 1) & 7))) << 3)));
                     acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], acc_s, 0, 0, 0);
                 }
                 s[2 * half + i] = acc_s;
@@ -439,67 +453,92 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const float p = s[i][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i][r] - mref);
                 lsum += p;
-                if (l16 < G) p_lds[wave][16 * i + 4 * grp + r][l16] = p;
+                s[i][r] = p;
             }
         lsum += __shfl_xor(lsum, 16, 64);
         lsum += __shfl_xor(lsum, 32, 64);
         m_w = mx;
         l_w = lsum;
-        __builtin_amdgcn_wave_barrier();
-        // O[head, d] += p[head, token] V[token, d]: lane owns dims 8 l16 .. +7 of
-        // tokens 4k + grp
+        // O^T[d, head] = V^T[d, tokens] . P^T[tokens, head] on v_mfma_f32_16x16x32_bf16,
+        // 32 tokens per step.  The k order of both operands: slot j of lane group
+        // grp is token 16 (j / 4) + 4 grp + j % 4 of the step, which is where the
+        // score accumulator left this lane's p (head l16), so P^T needs no shuffle.
+        // P enters as bf16 hi + lo halves (two MFMAs), a 16-bit significand: the
+        // products keep f32-grade accuracy, as the reference's f32 weights do.
+        bf16x8_t ph[2], pl[2];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const uint32_t keep = ((live >> (4 * k + grp)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
-            float v[8];
-            if constexpr (BF) {
-                uint4 w = vb[k];
-                w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
-                unpack_vec<PUTER_BF16>(w, v);
-            } else {
-                const uint32_t w[2] = {vb[k].x & keep, vb[k].y & keep};
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], false);
-                    const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], true);
-                    v[4 * q] = f0[0]; v[4 * q + 1] = f0[1]; v[4 * q + 2] = f1[0]; v[4 * q + 3] = f1[1];
-                }
-            }
-            float p[G];
-#pragma unroll
-            for (int h = 0; h < G; ++h) p[h] = p_lds[wave][4 * k + grp][h];
-#pragma unroll
-            for (int h = 0; h < G; ++h)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(p[h], v[j], acc[h][j]);
-        }
-        // sum the 4 token groups: every lane row then holds the wave's totals
-#pragma unroll
-        for (int h = 0; h < G; ++h)
+        for (int st = 0; st < 2; ++st)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                float v = acc[h][j];
-                const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-                v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-                const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-                acc[h][j] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+                const float p = s[2 * st + (j >> 2)][j & 3];
+                const __bf16 hi = (__bf16)p;
+                ph[st][j] = hi;
+                pl[st][j] = (__bf16)(p - (float)hi);
             }
+        f32x4_t ot[8];
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) ot[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        // V^T from the wave's tile: row r (token of the step) keeps its 16-byte
+        // chunk c at c ^ 2 (r % 8), so the transposing reads below (4 rows x 32
+        // bytes per 16 lanes) hit distinct banks.  Lane l16 of group grp reads row
+        // 4 grp + l16 / 4 (and + 16), dims 16 mt + 4 (l16 % 4) .. + 3; within the
+        // 16 lanes the read hands lane i dims 16 mt + i of those 4 rows.
+        const int vr = 4 * grp + (l16 >> 2);
+        const int vq = l16 & 3;   // dims 4 vq .. + 3 of the 32-byte run: 8-byte unit vq
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            __builtin_amdgcn_wave_barrier();   // the tile's previous reads are done
+            if constexpr (BF) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int kk = 8 * st + k, r = 4 * k + grp;
+                    const uint32_t keep = ((live >> (4 * kk + grp)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
+                    const uint4 w = make_uint4(vb[kk].x & keep, vb[kk].y & keep, vb[kk].z & keep, vb[kk].w & keep);
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + ((l16 ^ (2 * (r & 7))) << 4)) = w;
+                }
+            } else {   // 16 fp8 codes (dims 16 l8 .. + 15) -> two bf16 pieces 2 l8, 2 l8 + 1
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int kk = 4 * st + k, r = 8 * k + g8;
+                    const uint32_t keep = ((live >> (8 * kk + g8)) & 1) ? 0xFFFFFFFFu : 0u;
+                    const uint4 w0 = fp8x8_to_bf16(make_uint2(vb[kk].x & keep, vb[kk].y & keep));
+                    const uint4 w1 = fp8x8_to_bf16(make_uint2(vb[kk].z & keep, vb[kk].w & keep));
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8) ^ (2 * (r & 7))) << 4)) = w0;
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8 + 1) ^ (2 * (r & 7))) << 4)) = w1;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int mt = 0; mt < 8; ++mt) {
+                const int unit = ((2 * mt + (vq >> 1)) ^ (2 * (vr & 7))) * 2 + (vq & 1);   // 8-byte unit in the row
+                const char *p = tile + vr * 256 + unit * 8;
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 16 * 256));
+                const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[st], ot[mt], 0, 0, 0);
+                ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[st], ot[mt], 0, 0, 0);
+            }
+        }
+        // lane (grp, l16): O[head l16][16 mt + 4 grp + r] = ot[mt][r]
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[mt][r] = ot[mt][r];
     }
     // merge the four waves: (m, l) per head and o[head][128] through LDS (the o
-    // rows reuse the K tiles, so every wave must be done with its tile first)
+    // rows reuse the tiles, so every wave must be done with its tile first)
     __syncthreads();
     float *o_lds = reinterpret_cast<float *>(&k_lds[0][0]);   // [4][G][128]
     if (grp == 0 && l16 < G) {
         ml_lds[wave][l16][0] = m_w;
         ml_lds[wave][l16][1] = l_w;
     }
+    if (l16 < G) {
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-        if ((h & 3) == grp) {
-            float4 *dst = reinterpret_cast<float4 *>(o_lds + (wave * G + h) * D + 8 * l16);
-            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-        }
+        for (int mt = 0; mt < 8; ++mt)
+            *reinterpret_cast<float4 *>(o_lds + (wave * G + l16) * D + 16 * mt + 4 * grp) =
+                make_float4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]);
+    }
     __syncthreads();
     const int64_t slot0 = ((int64_t)b * a.heads + (int64_t)kvh * G) * a.max_splits + split;
     for (int idx = tid; idx < G * D; idx += 256) {
