@@ -60,20 +60,18 @@ struct DecodeArgs {
     float scale;
 };
 
-// 8 fp8-E4M3 codes (8 bytes) -> 8 bf16.  The hardware v_cvt_pk_f32_fp8 decodes
-// OCP E4M3FN on gfx950 (exact for every code); every E4M3 value is also a bf16
-// value, so the narrowing to bf16 is exact too.
+// 8 fp8-E4M3 codes (8 bytes) -> 8 bf16, two codes per v_cvt_scalef32_pk_bf16_fp8
+// (OCP E4M3FN, scale 1).  Every E4M3 value is a bf16 value; on MI355X this
+// instruction gives the same bf16 bits as the exact v_cvt_pk_f32_fp8 widening
+// narrowed to bf16, for all 65536 code pairs (NaN for NaN), in half the
+// instructions.
 __device__ __forceinline__ uint4 fp8x8_to_bf16(uint2 raw) {
     const uint32_t w[2] = {raw.x, raw.y};
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);  // bytes 0, 1
-        const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);   // bytes 2, 3
-        const bf16x2_t h0 = {(__bf16)f0[0], (__bf16)f0[1]};
-        const bf16x2_t h1 = {(__bf16)f1[0], (__bf16)f1[1]};
-        o[2 * k] = __builtin_bit_cast(uint32_t, h0);
-        o[2 * k + 1] = __builtin_bit_cast(uint32_t, h1);
+        o[2 * k] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[k], 1.0f, false));     // bytes 0, 1
+        o[2 * k + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[k], 1.0f, true));  // bytes 2, 3
     }
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
@@ -330,7 +328,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 // in one process on the configs[4] pool against the sub-chunk walk: bf16 +1%,
 // fp8 +4%; MFMA P.V with 16-byte fp8 row pieces then took fp8 from 144.6 to
 // 138.0 us (bf16 unchanged).
-template <int KV, int G>
+template <int KV, int G, bool O32>
 __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     constexpr int D = 128, TW = 64;
     constexpr bool BF = KV == PUTER_BF16;
@@ -378,9 +376,15 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 #pragma unroll
         for (int k = 0; k < NL; ++k) {
             const int row = max(__shfl(myrow, BF ? 4 * k + grp : 8 * k + g8, 64), 0);
-            const int64_t off = ((int64_t)row * inner + head_off) * EB + 16 * (BF ? l16 : l8);
-            kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
-            vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
+            if constexpr (O32) {   // pools under 4 GiB: 32-bit offsets from the pool base
+                const uint32_t off = (uint32_t)row * (uint32_t)(inner * EB) + (uint32_t)(head_off * EB) + 16u * (BF ? l16 : l8);
+                kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
+                vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
+            } else {
+                const int64_t off = ((int64_t)row * inner + head_off) * EB + 16 * (BF ? l16 : l8);
+                kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
+                vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
+            }
         }
         // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero
         bf16x8_t qb[4];
@@ -393,6 +397,9 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
         }
         const uint64_t live = __ballot(myrow >= 0);   // token t live iff bit t
         char *tile = k_lds[wave];
+        // every token live (the common case below a sequence's last 64 tokens):
+        // the mask tests below are skipped (wave-uniform branches)
+        const bool full = live == ~0ull;
         // scores S^T[token, head], 32 tokens at a time: K rows -> the wave's LDS
         // tile, then A = tile rows 16i + l16, B = Q^T; lane: head l16, tokens
         // 16i + 4grp + r.  bf16 rows keep 16-byte piece c at c ^ (r % 16); fp8 rows
@@ -439,10 +446,20 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
             for (int r = 0; r < 4; ++r) {
                 float v = s[i][r];
                 if constexpr (BF) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
-                v = ((live >> (16 * i + 4 * grp + r)) & 1) ? v * c : -INFINITY;
-                s[i][r] = v;
-                mx = fmaxf(mx, v);
+                s[i][r] = v * c;
             }
+        if (!full) {
+            const uint64_t lg = live >> (4 * grp);   // bit 16i + r: token 16i + 4grp + r
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (!((lg >> (16 * i + r)) & 1)) s[i][r] = -INFINITY;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[i][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mref = mx == -INFINITY ? 0.0f : mx;
@@ -451,7 +468,8 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = s[i][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i][r] - mref);
+                // exp2(-inf - mref) is exactly 0 for a dead token (mref finite)
+                const float p = __builtin_amdgcn_exp2f(s[i][r] - mref);
                 lsum += p;
                 s[i][r] = p;
             }
@@ -492,17 +510,24 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const int kk = 8 * st + k, r = 4 * k + grp;
-                    const uint32_t keep = ((live >> (4 * kk + grp)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
-                    const uint4 w = make_uint4(vb[kk].x & keep, vb[kk].y & keep, vb[kk].z & keep, vb[kk].w & keep);
+                    uint4 w = vb[kk];
+                    if (!full) {   // dead rows: exact zeros
+                        const uint32_t keep = ((live >> (4 * kk + grp)) & 1) ? 0xFFFFFFFFu : 0u;
+                        w = make_uint4(w.x & keep, w.y & keep, w.z & keep, w.w & keep);
+                    }
                     *reinterpret_cast<uint4 *>(tile + r * 256 + ((l16 ^ (2 * (r & 7))) << 4)) = w;
                 }
             } else {   // 16 fp8 codes (dims 16 l8 .. + 15) -> two bf16 pieces 2 l8, 2 l8 + 1
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int kk = 4 * st + k, r = 8 * k + g8;
-                    const uint32_t keep = ((live >> (8 * kk + g8)) & 1) ? 0xFFFFFFFFu : 0u;
-                    const uint4 w0 = fp8x8_to_bf16(make_uint2(vb[kk].x & keep, vb[kk].y & keep));
-                    const uint4 w1 = fp8x8_to_bf16(make_uint2(vb[kk].z & keep, vb[kk].w & keep));
+                    uint4 raw = vb[kk];
+                    if (!full) {
+                        const uint32_t keep = ((live >> (8 * kk + g8)) & 1) ? 0xFFFFFFFFu : 0u;
+                        raw = make_uint4(raw.x & keep, raw.y & keep, raw.z & keep, raw.w & keep);
+                    }
+                    const uint4 w0 = fp8x8_to_bf16(make_uint2(raw.x, raw.y));
+                    const uint4 w1 = fp8x8_to_bf16(make_uint2(raw.z, raw.w));
                     *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8) ^ (2 * (r & 7))) << 4)) = w0;
                     *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8 + 1) ^ (2 * (r & 7))) << 4)) = w1;
                 }
@@ -733,17 +758,24 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
         return check_launch("paged decode");
     }
     const dim3 grid((unsigned)kv_heads, (unsigned)splits, (unsigned)batch);
-#define PUTER_DECODE(KV)                                                              \
+    // pools under 4 GiB take 32-bit row offsets
+    const bool o32 = (uint64_t)num_pages * (uint64_t)page_size * (uint64_t)kv_heads * (uint64_t)head_dim *
+                         (kv_dtype == PUTER_BF16 ? 2u : 1u) < ((uint64_t)1 << 32);
+#define PUTER_DECODE_G(KV, O)                                                         \
     switch (G) {                                                                      \
-    case 1: decode_block_kernel<KV, 1><<<grid, 256, 0, s>>>(a); break;                \
-    case 2: decode_block_kernel<KV, 2><<<grid, 256, 0, s>>>(a); break;                \
-    case 4: decode_block_kernel<KV, 4><<<grid, 256, 0, s>>>(a); break;                \
-    case 8: decode_block_kernel<KV, 8><<<grid, 256, 0, s>>>(a); break;                \
-    }                                                                                 \
+    case 1: decode_block_kernel<KV, 1, O><<<grid, 256, 0, s>>>(a); break;             \
+    case 2: decode_block_kernel<KV, 2, O><<<grid, 256, 0, s>>>(a); break;             \
+    case 4: decode_block_kernel<KV, 4, O><<<grid, 256, 0, s>>>(a); break;             \
+    case 8: decode_block_kernel<KV, 8, O><<<grid, 256, 0, s>>>(a); break;             \
+    }
+#define PUTER_DECODE(KV)                                                              \
+    if (o32) { PUTER_DECODE_G(KV, true) }                                             \
+    else { PUTER_DECODE_G(KV, false) }                                                \
     decode_combine_kernel<KV><<<dim3((unsigned)num_heads, (unsigned)batch), 128, 0, s>>>(a);
     if (kv_dtype == PUTER_BF16) { PUTER_DECODE(PUTER_BF16) }
     else { PUTER_DECODE(PUTER_F8E4M3) }
 #undef PUTER_DECODE
+#undef PUTER_DECODE_G
     return check_launch("paged decode");
 }
 

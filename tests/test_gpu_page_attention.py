@@ -416,6 +416,30 @@ def test_paged_decode(backend, kv_dt, batch, lo, hi, ps):
                  elem_tol=None, what="paged decode")
 
 
+def test_paged_decode_fp8_value_codes_exact(backend):
+    """One live token per sequence: its softmax weight is exactly 1, so the output
+    is the token's V row widened from fp8 and narrowed to bf16, bit for bit.  Two
+    sequences hold all 256 E4M3 codes in their V rows (NaN codes give NaN), which
+    pins the kernel's fp8 -> bf16 widening code by code (convert/fp8_f32.go)."""
+    h = kvh = 1
+    d, ps = 128, 16
+    ctx = np.array([1, 1], np.int32)
+    table = np.array([[0], [1]], np.int32)
+    q = O.from_f32(seeded(5, (2, h * d)), O.BF16)
+    kp = np.zeros((2, ps, kvh, d), np.uint8)
+    vp = np.zeros((2, ps, kvh, d), np.uint8)
+    codes = np.arange(256, dtype=np.uint8)
+    vp[0, 0, 0] = codes[:128]
+    vp[1, 0, 0] = codes[128:]
+    ks = vs = np.ones(kvh, np.float32)
+    out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, 2, h, kvh, d, O.F8E4M3, ks, vs)
+    got = O.to_f32(out.reshape(-1), O.BF16)
+    want = O.to_f32(codes, O.F8E4M3)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])   # -0 sums to +0, as the reference's 0 + 1 * v does
+
+
 # group sizes 1, 2, 8 and page sizes that do not divide the 32-token sub-chunks
 @pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
 @pytest.mark.parametrize("h,kvh", [(8, 8), (8, 4), (16, 2)])
