@@ -18,9 +18,20 @@ HIP kernels register under the device location the dispatcher already routes
 Only kernels whose behaviour is fixed by their tensors are registered (Run takes
 tensors, no config): paged KV write / gather (the reference's own registered
 names), LayerNorm (its epsilon is fixed at 1e-5, device/cpu/layernorm/compute.go:11),
-the gated activations in tensor form, Silu / Gelu, the dtype casts and Matmul.
-Ops that carry a config (RMSNorm epsilon, RoPE, MultiHeadAttention) are reached
-through the device.Backend methods, as the reference's dispatcher reaches them.
+the gated activations in tensor form, Silu / Gelu, the dtype casts, Matmul, and
+the names the reference's CPU backend registers with default configs on this
+path: multi_head_attention / grouped_query_attention / sliding_window_attention
+(NumHeads 8, HeadDim 64; KV heads 2 for GQA; causal, window 128 for the sliding
+one: device/cpu/attention/attention_variants.go:27-60,
+attention_variants_dtype.go:14-25, registered at
+device/cpu/neon/remaining_ops_dtype.go:252-290,737-777), attention /
+flash_attention (single head, BlockSize 64, not causal: attention.go:141-152,
+flash_attention.go:38-40,132-141), int8_dequant / int4_dequant / int8_quant
+(scale 1, zero point 0: dequant/tensor.go:7-21, quant/tensor.go:8-14,
+dequant/config.go:13-19; remaining_ops_dtype.go:647-665).  Ops that carry a
+caller's config (RMSNorm epsilon, RoPE, MultiHeadAttention with other heads)
+are reached through the device.Backend methods, as the reference's dispatcher
+reaches them.
 """
 from dataclasses import dataclass, field
 import threading
@@ -34,10 +45,10 @@ LOCATION_DEVICE = "cuda"        # tensor.CUDA: the device location HIP kernels r
 
 # dtype names of manifesto/dtype for the formats on the path, mapped to the
 # library's codes
-F32, F16, BF16, F8E4M3, F8E5M2, I32, I8, F64 = ("float32", "float16", "bfloat16", "float8e4m3",
-                                               "float8e5m2", "int32", "int8", "float64")
+F32, F16, BF16, F8E4M3, F8E5M2, I32, I8, I4, F64 = ("float32", "float16", "bfloat16", "float8e4m3",
+                                                   "float8e5m2", "int32", "int8", "int4", "float64")
 _CODE = {F32: _be.F32, F16: _be.F16, BF16: _be.BF16, F8E4M3: _be.F8E4M3, F8E5M2: _be.F8E5M2,
-         I32: _be.I32, I8: _be.I8, F64: _be.F64}
+         I32: _be.I32, I8: _be.I8, I4: _be.I4, F64: _be.F64}
 
 
 class RegistryError(RuntimeError):
@@ -220,6 +231,76 @@ def _matmul(be, dt):
     return run
 
 
+# the reference's default attention configs (attention_variants.go:27-60,
+# attention_variants_dtype.go:14-25)
+ATTENTION_VARIANTS = (("multi_head_attention", dict()),
+                      ("grouped_query_attention", dict(KVHeadCount=2)),
+                      ("sliding_window_attention", dict(Causal=True, WindowSize=128)))
+
+
+def _mha_default(be, dt, overrides):
+    """args: query [seqQ, 8*64], key, value [seqK, kvHeads*64], out [seqQ, 8*64]
+    (multiHeadAttentionMixedDims, attention_variants_dtype.go:27-64)."""
+    cfg = _be.MultiHeadAttentionConfig(NumHeads=8, HeadDim=64, **overrides)
+    kvh = cfg.KVHeadCount if cfg.KVHeadCount > 0 else cfg.NumHeads
+
+    def run(*args):
+        if len(args) != 4:
+            raise _mismatch()
+        q, k, v, out = args
+        if any(t.dim() != 2 for t in args):
+            raise _mismatch()
+        qf, kf = cfg.NumHeads * cfg.HeadDim, kvh * cfg.HeadDim
+        if q.shape[1] != qf or k.shape[1] != kf or v.shape[1] != kf or out.shape[1] != qf:
+            raise _mismatch()
+        be.MultiHeadAttention(cfg, q, k, v, out, int(q.shape[0]), int(k.shape[0]), _CODE[dt])
+    return run
+
+
+def _flash_default(be, dt):
+    """args: query [seqQ, depth], key [seqK, depth], value [seqK, valueDim], out
+    [seqQ, valueDim]; BlockSize 64, not causal (attentionViews, attention.go:154-...)."""
+    cfg = _be.FlashAttentionConfig(BlockSize=64, Causal=False)
+
+    def run(*args):
+        if len(args) != 4 or any(t.dim() != 2 for t in args):
+            raise _mismatch()
+        q, k, v, out = args
+        sq, depth, sk, vd = int(q.shape[0]), int(q.shape[1]), int(k.shape[0]), int(v.shape[1])
+        if k.shape[1] != depth or v.shape[0] != sk or out.shape[0] != sq or out.shape[1] != vd:
+            raise _mismatch()
+        be.FlashAttention(cfg, q, k, v, out, sq, sk, depth, vd, _CODE[dt])
+    return run
+
+
+def _int8_dequant(be):
+    """args: quantized int8, output f32 of the same length; scale 1, zero point 0."""
+    def run(*args):
+        if len(args) != 2 or args[0].numel() != args[1].numel():
+            raise _mismatch()
+        be.Dequant(args[1], args[0], args[0].numel(), _be.DequantInt8Config(1.0, 0), _be.F32, _be.I8)
+    return run
+
+
+def _int4_dequant(be):
+    """args: packed int4 (two codes per byte, low nibble first), output f32 of at
+    most twice the byte count; scale 1, zero point 0 (dequant/tensor.go:48-73)."""
+    def run(*args):
+        if len(args) != 2 or args[1].numel() > 2 * args[0].numel():
+            raise _mismatch()
+        be.Dequant4(args[1], args[0], args[1].numel(), _be.DequantInt4Config(1.0, 0), _be.F32, _be.I4)
+    return run
+
+
+def _int8_quant(be):
+    """args: input f32, output int8 of the same length; scale 1, zero point 0."""
+    def run(*args):
+        if len(args) != 2 or args[0].numel() != args[1].numel():
+            raise _mismatch()
+        be.Quant(args[1], args[0], args[0].numel(), _be.DequantInt8Config(1.0, 0), _be.I8, _be.F32)
+    return run
+
+
 GATED = (("swiglu", "SwiGLUTensors"), ("geglu", "GeGLUTensors"), ("geglu_tanh", "GeGLUTanhTensors"),
          ("siglu", "SiGLUTensors"), ("glu", "GLUTensors"), ("reglu", "ReGLUTensors"),
          ("linglu", "LinGLUTensors"))
@@ -254,4 +335,12 @@ def register_hip_kernels(registry: Registry = None, backend=None) -> Registry:
                 reg("cast", [src], [dst], _cast(be, src, dst))
     reg("cast", [I8], [F32], _cast(be, I8, F32))
     reg("cast", [F32], [I8], _cast(be, F32, I8))
+    for dt in (F32, BF16, F16):
+        for name, overrides in ATTENTION_VARIANTS:
+            reg(name, [dt, dt, dt], [dt], _mha_default(be, dt, overrides))
+        reg("attention", [dt, dt, dt], [dt], _flash_default(be, dt))
+        reg("flash_attention", [dt, dt, dt], [dt], _flash_default(be, dt))
+    reg("int8_dequant", [I8], [F32], _int8_dequant(be))
+    reg("int4_dequant", [I4], [F32], _int4_dequant(be))
+    reg("int8_quant", [F32], [I8], _int8_quant(be))
     return registry

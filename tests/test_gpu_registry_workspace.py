@@ -73,6 +73,58 @@ def test_registry_layernorm_swiglu_cast_matmul(backend, reg):
     assert_close(to_host(c, np.float32), O.matmul_f32(a, w), TOL[O.F32], elem_tol=1e-3, what="matmul")
 
 
+@pytest.mark.parametrize("name,kw", [("multi_head_attention", dict(causal=False)),
+                                     ("grouped_query_attention", dict(causal=False, kv_heads=2)),
+                                     ("sliding_window_attention", dict(causal=True, window=128))])
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+def test_registry_attention_defaults(backend, reg, name, kw, dt):
+    """The reference's registered attention names with their default configs
+    (8 heads of 64; GQA over 2 kv heads; causal sliding window 128), looked up
+    and run on device tensors, against the oracle's MultiHeadAttention."""
+    import torch
+    R = reg[0]
+    rdt = {O.F32: R.F32, O.BF16: R.BF16}[dt]
+    tdt = {O.F32: torch.float32, O.BF16: torch.bfloat16}[dt]
+    kvh = kw.get("kv_heads", 8)
+    sq, sk = 200, 200
+    q = O.from_f32(seeded(11, (sq, 8 * 64), 0.0, 0.5), dt)
+    k = O.from_f32(seeded(12, (sk, kvh * 64), 0.0, 0.5), dt)
+    v = O.from_f32(seeded(13, (sk, kvh * 64)), dt)
+    dev = lambda a: to_dev(a).view(tdt)  # noqa: E731
+    out = torch.empty((sq, 8 * 64), dtype=tdt, device="cuda")
+    _lookup(reg, name, [rdt] * 3, [rdt])(dev(q), dev(k), dev(v), out)
+    ref = O.to_f32(O.mha(q, k, v, 8, 64, causal=kw["causal"], kv_heads=kw.get("kv_heads", 0),
+                         window=kw.get("window", 0), dtype=dt), dt)
+    got = O.to_f32(to_host(out.view(torch.int16) if dt == O.BF16 else out,
+                           np.uint16 if dt == O.BF16 else np.float32), dt)
+    assert_close(got, ref, TOL[dt], elem_tol=None if dt == O.BF16 else 1e-3, what=name)
+    with pytest.raises(Exception):      # a query width other than 8 x 64: ErrShapeMismatch
+        _lookup(reg, name, [rdt] * 3, [rdt])(dev(q)[:, :256], dev(k), dev(v), out[:, :256])
+
+
+def test_registry_flash_attention_and_quant(backend, reg):
+    import torch
+    R = reg[0]
+    q, k, v = seeded(14, (37, 48)), seeded(15, (90, 48)), seeded(16, (90, 24))
+    out = torch.empty((37, 24), dtype=torch.float32, device="cuda")
+    for name in ("attention", "flash_attention"):
+        _lookup(reg, name, [R.F32] * 3, [R.F32])(to_dev(q), to_dev(k), to_dev(v), out)
+        assert_close(to_host(out, np.float32), O.flash_attention(q, k, v, causal=False), TOL[O.F32],
+                     elem_tol=1e-3, what=name)
+    x = (seeded(17, (4097,)) * 60.0).astype(np.float32)
+    codes = torch.empty(4097, dtype=torch.int8, device="cuda")
+    _lookup(reg, "int8_quant", [R.F32], [R.I8])(to_dev(x), codes)
+    want = O.quant_int8(x, 1.0, 0)
+    assert np.array_equal(to_host(codes, np.int8), want)
+    back = torch.empty(4097, dtype=torch.float32, device="cuda")
+    _lookup(reg, "int8_dequant", [R.I8], [R.F32])(codes, back)
+    assert np.array_equal(to_host(back, np.float32), O.dequant_int8(want, 1.0, 0))
+    packed = np.random.default_rng(18).integers(0, 256, 2049).astype(np.uint8)
+    out4 = torch.empty(4097, dtype=torch.float32, device="cuda")
+    _lookup(reg, "int4_dequant", [R.I4], [R.F32])(to_dev(packed), out4)
+    assert np.array_equal(to_host(out4, np.float32), O.dequant_int4(packed, 4097, 1.0, 0))
+
+
 def test_workspace_slot_views_stay_resident(backend):
     """AllocateWorkspaceSlot / ViewWorkspaceSlot: one device allocation carved
     into views of other shapes and formats; a fused GatedResidual+RMSNorm reads
