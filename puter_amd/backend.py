@@ -184,6 +184,19 @@ class Backend:
         if v != 0:
             raise PuterError(v, "tensor: shape mismatch (page id or slot out of range)")
 
+    # execution/dispatch.go:120-123 (batchExecutionDevice): launches are already
+    # asynchronous on the backend's stream, so BeginBatch does nothing; EndBatch
+    # synchronises once and returns the status word's error (None when clear)
+    def BeginBatch(self):
+        return None
+
+    def EndBatch(self):
+        try:
+            self.CheckStatus()
+        except PuterError as e:
+            return e
+        return None
+
     # stream: explicit handle, else torch's current stream on the current device
     def stream(self):
         if self._stream is not None:

@@ -497,10 +497,13 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) ot[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
         // V^T from the wave's tile: row r (token of the step) keeps its 16-byte
-        // chunk c at c ^ 2 (r % 8), so the transposing reads below (4 rows x 32
-        // bytes per 16 lanes) hit distinct banks.  Lane l16 of group grp reads row
-        // 4 grp + l16 / 4 (and + 16), dims 16 mt + 4 (l16 % 4) .. + 3; within the
-        // 16 lanes the read hands lane i dims 16 mt + i of those 4 rows.
+        // chunk c at c ^ vsw(r), vsw(r) = 2 (r % 8) + r % 2: the transposing reads
+        // below (4 rows x 32 bytes per 16 lanes) hit distinct banks, and so do the
+        // fp8 writes (two rows' even chunks per 16 lanes land on opposite chunk
+        // parities).  Lane l16 of group grp reads row 4 grp + l16 / 4 (and + 16),
+        // dims 16 mt + 4 (l16 % 4) .. + 3; within the 16 lanes the read hands
+        // lane i dims 16 mt + i of those 4 rows.
+        auto vsw = [](int r) { return (2 * (r & 7)) | (r & 1); };
         const int vr = 4 * grp + (l16 >> 2);
         const int vq = l16 & 3;   // dims 4 vq .. + 3 of the 32-byte run: 8-byte unit vq
 #pragma unroll
@@ -515,7 +518,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                         const uint32_t keep = ((live >> (4 * kk + grp)) & 1) ? 0xFFFFFFFFu : 0u;
                         w = make_uint4(w.x & keep, w.y & keep, w.z & keep, w.w & keep);
                     }
-                    *reinterpret_cast<uint4 *>(tile + r * 256 + ((l16 ^ (2 * (r & 7))) << 4)) = w;
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + ((l16 ^ vsw(r)) << 4)) = w;
                 }
             } else {   // 16 fp8 codes (dims 16 l8 .. + 15) -> two bf16 pieces 2 l8, 2 l8 + 1
 #pragma unroll
@@ -528,14 +531,14 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                     }
                     const uint4 w0 = fp8x8_to_bf16(make_uint2(raw.x, raw.y));
                     const uint4 w1 = fp8x8_to_bf16(make_uint2(raw.z, raw.w));
-                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8) ^ (2 * (r & 7))) << 4)) = w0;
-                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8 + 1) ^ (2 * (r & 7))) << 4)) = w1;
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8) ^ vsw(r)) << 4)) = w0;
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8 + 1) ^ vsw(r)) << 4)) = w1;
                 }
             }
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt) {
-                const int unit = ((2 * mt + (vq >> 1)) ^ (2 * (vr & 7))) * 2 + (vq & 1);   // 8-byte unit in the row
+                const int unit = ((2 * mt + (vq >> 1)) ^ vsw(vr)) * 2 + (vq & 1);   // 8-byte unit in the row
                 const char *p = tile + vr * 256 + unit * 8;
                 const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
                 const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 16 * 256));

@@ -147,6 +147,13 @@ def test_page_out_of_range_ids_never_touch_memory(backend):
     # a valid call leaves the word clear
     backend.KVPageGather(d, to_dev(np.array([1, 3], np.int32)), out, pages, ps, inner, 2 * ps, 0, O.F32)
     backend.CheckStatus()
+    # the batching hooks (execution/dispatch.go:120-123): EndBatch returns the
+    # batch's page error instead of raising, and clears it
+    assert backend.BeginBatch() is None
+    backend.KVPageGather(d, to_dev(np.array([5], np.int32)), out, pages, ps, inner, ps, 0, O.F32)
+    err = backend.EndBatch()
+    assert isinstance(err, puter_amd.PuterError) and err.status == -6
+    assert backend.EndBatch() is None
 
 
 @pytest.mark.parametrize("dt,inner,rows", [(O.BF16, 1024, 300), (O.F32, 3, 77), (O.F8E4M3, 1024, 200),
