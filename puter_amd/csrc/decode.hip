@@ -93,19 +93,19 @@ __device__ __forceinline__ void f16x8_to_f32(const uint4 &w, float (&v)[8]) {
 // have landed and its K rows are parked in LDS, sub-chunk n+1's K and V rows
 // are loaded (V into a second register set) while n is computed, so every wave
 // keeps a sub-chunk of loads in flight while it works; small registers and LDS
-// let 8 waves share a CU.  Every load instruction
-// reads whole KV rows: lane group grp takes token 4k + grp, lane l16 its 16-byte
-// (bf16) or 8-byte (fp8) piece l16.  K rows then pass through a wave-private
-// LDS tile (piece p of row r stored at p ^ swizzle(r)) to reach the MFMA
-// operand layout, 16 rows x one piece per read, bank-conflict free.
+// let 8 waves share a CU.  Every load instruction reads whole KV rows: lane
+// group grp takes token 4k + grp, lane l16 its 16-byte piece l16.  K rows then
+// pass through a wave-private LDS tile (piece p of row r stored at p ^ (r % 16))
+// to reach the MFMA operand layout, 16 rows x one piece per read, bank-conflict
+// free.  One-row MultiHeadAttention runs it over bf16 or f16 K/V (KV).
 template <int KV, int G, int SPLIT = kSplit>
 __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a) {
     constexpr int D = 128, SUB = 32, NSUB = SPLIT / SUB, NGRP = (SPLIT + 63) / 64;
+    static_assert(KV == PUTER_BF16 || KV == PUTER_F16, "16-bit K/V only");
     constexpr bool BF = KV == PUTER_BF16;
-    constexpr bool H16 = KV == PUTER_F16;         // f16 K/V and query (one-row attention)
-    constexpr bool W16 = BF || H16;               // 16-bit K/V rows
-    constexpr int RB = W16 ? 256 : 128;           // KV row bytes
-    using VT = typename std::conditional<W16, uint4, uint2>::type;
+    constexpr bool H16 = KV == PUTER_F16;         // f16 K/V and query
+    constexpr int RB = 256;                       // KV row bytes
+    using VT = uint4;
     __shared__ __attribute__((aligned(1024))) char k_lds[SUB * RB];
     __shared__ float p_lds[SUB][G];               // probabilities [token][head]
 
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
     const int64_t head_off = (int64_t)kvh * D;
     const uint8_t *kpool = static_cast<const uint8_t *>(a.kp);
     const uint8_t *vpool = static_cast<const uint8_t *>(a.vp);
-    constexpr int EB = W16 ? 2 : 1;
+    constexpr int EB = 2;
     // byte offset of this lane's piece of pool row `row`
     auto piece = [&](int row) -> int64_t { return ((int64_t)row * inner + head_off) * EB + (int64_t)sizeof(VT) * l16; };
 
@@ -160,18 +160,12 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int64_t off = piece(max(__shfl(src, base + 4 * k + grp, 64), 0));
-            if constexpr (W16) {
-                kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
-                vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
-            } else {
-                kb[k] = *reinterpret_cast<const uint2 *>(kpool + off);
-                vb[k] = *reinterpret_cast<const uint2 *>(vpool + off);
-            }
+            kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
+            vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
         }
     };
 
-    const float kscale = W16 ? 1.0f : a.ks[kvh];
-    const float c = a.scale * kscale * 1.4426950408889634f;
+    const float c = a.scale * 1.4426950408889634f;
     float m_run = -INFINITY, l_run = 0.0f;   // head l16's running max (log2 domain) and sum
     float acc[G][8];
 #pragma unroll
@@ -191,8 +185,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int r = 4 * k + grp;
-            if constexpr (W16) *reinterpret_cast<uint4 *>(k_lds + r * 256 + ((l16 ^ (r & 15)) << 4)) = kbuf[k];
-            else *reinterpret_cast<uint2 *>(k_lds + r * 128 + ((l16 ^ ((r >> 1) & 7)) << 3)) = kbuf[k];
+            *reinterpret_cast<uint4 *>(k_lds + r * 256 + ((l16 ^ (r & 15)) << 4)) = kbuf[k];
         }
         if (n + 1 < NSUB) issue(n + 1, kbuf, vbuf[(n + 1) & 1]);
         __builtin_amdgcn_wave_barrier();   // the tile is private to this wave; LDS ops run in order
@@ -208,13 +201,7 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
             const int row = 16 * i + l16;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                uint4 kv;
-                if constexpr (W16) {
-                    kv = *reinterpret_cast<const uint4 *>(k_lds + row * 256 + (((4 * t + grp) ^ l16) << 4));
-                } else {
-                    kv = fp8x8_to_bf16(*reinterpret_cast<const uint2 *>(
-                        k_lds + row * 128 + (((4 * t + grp) ^ ((l16 >> 1) & 7)) << 3)));
-                }
+                const uint4 kv = *reinterpret_cast<const uint4 *>(k_lds + row * 256 + (((4 * t + grp) ^ l16) << 4));
                 if constexpr (H16)
                     s[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, kv),
                                                                   __builtin_bit_cast(f16x8_t, qb[t]), s[i], 0, 0, 0);
@@ -265,20 +252,10 @@ __global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a
         for (int k = 0; k < 8; ++k) {
             const uint32_t keep = ((livev >> (4 * k)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
             float v[8];
-            if constexpr (W16) {
-                uint4 w = vc[k];
-                w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
-                if constexpr (H16) f16x8_to_f32(w, v);
-                else unpack_vec<PUTER_BF16>(w, v);
-            } else {   // E4M3 widened straight to f32 (the same values as through bf16)
-                const uint32_t w[2] = {vc[k].x & keep, vc[k].y & keep};
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], false);  // bytes 0, 1
-                    const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], true);   // bytes 2, 3
-                    v[4 * q] = f0[0]; v[4 * q + 1] = f0[1]; v[4 * q + 2] = f1[0]; v[4 * q + 3] = f1[1];
-                }
-            }
+            uint4 w = vc[k];
+            w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
+            if constexpr (H16) f16x8_to_f32(w, v);
+            else unpack_vec<PUTER_BF16>(w, v);
             float p[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) p[h] = p_lds[4 * k + grp][h];
