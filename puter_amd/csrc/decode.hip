@@ -569,42 +569,44 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 }
 
 // One (query head, sequence) per block, one output dim per thread: merge the
-// sequence's split partials by log-sum-exp.  The (m, l) pairs are read by
-// all threads (the same addresses: one transaction), the split loop is
-// unrolled 4-wide so its loads are in flight together.
+// sequence's split partials by log-sum-exp in one pass over batches of 16
+// splits.  Every (m, l) and o load of a batch is issued before any is used (the
+// (m, l) pairs are the same addresses for all threads: one transaction), then the
+// batch folds into the running (M, L, O), rescaled when its max exceeds M; a
+// sequence of up to 16 splits is one round trip to memory.
 template <int KV, int SPLIT = kSplit>
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeArgs a) {
-    constexpr int D = 128;
+    constexpr int D = 128, NB = 16;
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int ctx = a.ctx ? (int)min((int64_t)a.ctx[b], a.max_context) : (int)a.max_context;
     const int nsplit = (ctx + SPLIT - 1) / SPLIT;
     const int64_t base = ((int64_t)b * a.heads + h) * a.max_splits;
     const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + base;
     const float *po = a.part_o + base * D + d;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[s].x);
-    float L = 0.0f, O = 0.0f;
-    int s = 0;
-    for (; s + 4 <= nsplit; s += 4) {
-        float2 m4[4];
-        float o4[4];
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += NB) {
+        float2 mv[NB];
+        float ov[NB];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            m4[u] = ml[s + u];
-            o4[u] = po[(int64_t)(s + u) * D];
+        for (int u = 0; u < NB; ++u) {
+            const bool in = s0 + u < nsplit;
+            mv[u] = in ? ml[s0 + u] : make_float2(-INFINITY, 0.0f);
+            ov[u] = in ? po[(int64_t)(s0 + u) * D] : 0.0f;
         }
+        float mb = M;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float f = m4[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m4[u].x - M);
-            L += m4[u].y * f;
-            O += o4[u] * f;
+        for (int u = 0; u < NB; ++u) mb = fmaxf(mb, mv[u].x);
+        if (mb == -INFINITY) continue;   // every split so far saw no live token
+        const float fo = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mb);
+        L *= fo;
+        O *= fo;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const float f = mv[u].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv[u].x - mb);
+            L += mv[u].y * f;
+            O += ov[u] * f;
         }
-    }
-    for (; s < nsplit; ++s) {
-        const float2 m1 = ml[s];
-        const float f = m1.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1.x - M);
-        L += m1.y * f;
-        O += po[(int64_t)s * D] * f;
+        M = mb;
     }
     float r = L > 0.0f ? O / L : 0.0f;
     if constexpr (KV == PUTER_F8E4M3) r *= a.vs[h / (a.heads / a.kv_heads)];
