@@ -56,6 +56,33 @@ def test_page_write_gather_roundtrip(backend, dt, inner):
     assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
 
 
+def test_page_write_gather_beyond_4gib(backend):
+    """A bf16 pool of more than 4 GiB (2 KiB rows): rows written to and gathered
+    from pages past the 4 GiB mark, bit-exact against the oracle on a compact
+    copy of those pages (the kernels index with 64-bit offsets)."""
+    import torch
+    ps, inner = 16, 1024
+    pages = (1 << 32) // (ps * inner * 2) + 64
+    far0 = pages - 8                                   # the last 8 pages
+    rng = np.random.default_rng(19)
+    vals = rng.integers(0, 1 << 16, (40, inner)).astype(np.uint16)
+    ids = rng.integers(0, 8, 40).astype(np.int32)
+    offs = rng.integers(0, ps, 40).astype(np.int32)
+    compact = rng.integers(0, 1 << 16, (8, ps, inner)).astype(np.uint16)
+    pool = torch.zeros((pages, ps, inner), dtype=torch.int16, device="cuda")
+    pool[far0:] = torch.from_numpy(compact.view(np.int16)).cuda()
+    backend.KVPageWrite(pool, to_dev(vals), to_dev(ids + far0), to_dev(offs), pool, pages, ps, inner, 40, 0, O.BF16)
+    want = O.page_write(compact.ravel(), vals, ids, offs, ps, inner).reshape(8, ps, inner)
+    assert np.array_equal(pool[far0:].cpu().numpy().view(np.uint16), want)
+    table = rng.permutation(8).astype(np.int32)
+    out = empty_dev((8 * ps, inner), np.uint16)
+    backend.KVPageGather(pool, to_dev(table + far0), out, pages, ps, inner, 8 * ps, 0, O.BF16)
+    assert np.array_equal(to_host(out, np.uint16), O.page_gather(want.ravel(), table, ps, inner, 8 * ps))
+    backend.CheckStatus()
+    del pool
+    torch.cuda.empty_cache()
+
+
 def test_page_gather_identity_table_is_contiguous_copy(backend):
     pages, ps, inner = 8, 4, 32
     storage = seeded(3, (pages * ps * inner,))
@@ -400,12 +427,14 @@ def paged_case(seed, batch, ctx_lo, ctx_hi, ps, h, kvh, d, kv_dt):
 
 
 def run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs):
+    """kp / vp: host arrays, or pools already on the device (torch tensors)."""
     batch = len(ctx)
     max_ctx = int(ctx.max())
     ws_bytes = backend.PagedDecodeWorkspaceBytes(batch, h, d, max_ctx)
     ws = empty_dev((ws_bytes // 4,), np.float32)
     out = empty_dev((batch, h * d), np.uint16)
-    backend.PagedDecodeAttention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(table), to_dev(ctx), batch,
+    dev = lambda x: x if hasattr(x, "data_ptr") else to_dev(x)  # noqa: E731
+    backend.PagedDecodeAttention(to_dev(q), dev(kp), dev(vp), to_dev(table), to_dev(ctx), batch,
                                  table.shape[1], ps, total, h, kvh, d, max_ctx,
                                  None if ks is None else to_dev(ks), None if vs is None else to_dev(vs),
                                  kv_dt, out, ws, ws_bytes)
@@ -421,6 +450,33 @@ def test_paged_decode(backend, kv_dt, batch, lo, hi, ps):
     out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
     assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
                  elem_tol=None, what="paged decode")
+
+
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+def test_paged_decode_pool_beyond_4gib(backend, kv_dt):
+    """Pools of more than 4 GiB take 64-bit row offsets (smaller ones 32-bit):
+    sequences whose pages lie past the 4 GiB mark of both pools, checked
+    against the oracle on a compact copy of those pages."""
+    import torch
+    h, kvh, d, ps = 32, 8, 128, 16
+    es = 2 if kv_dt == O.BF16 else 1
+    row_bytes = kvh * d * es
+    pages = (1 << 32) // (ps * row_bytes) + 2048           # just past 4 GiB per pool
+    ctx, table, total, q, kp, vp, ks, vs = paged_case(77, 2, 150, 400, ps, h, kvh, d, kv_dt)
+    far = (pages - total + np.arange(total)).astype(np.int32)   # compact page i -> pool page far[i]
+    big_table = far[table]
+    tdt = torch.int16 if kv_dt == O.BF16 else torch.uint8
+    npd = np.int16 if kv_dt == O.BF16 else np.uint8
+    kpool = torch.zeros((pages, ps, kvh, d), dtype=tdt, device="cuda")
+    vpool = torch.zeros((pages, ps, kvh, d), dtype=tdt, device="cuda")
+    idx = torch.from_numpy(far.astype(np.int64)).cuda()
+    kpool[idx] = torch.from_numpy(kp.view(npd)).cuda()
+    vpool[idx] = torch.from_numpy(vp.view(npd)).cuda()
+    ref = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, kv_dt, ks, vs)
+    out = run_paged_decode(backend, q, kpool, vpool, big_table, ctx, ps, pages, h, kvh, d, kv_dt, ks, vs)
+    del kpool, vpool
+    torch.cuda.empty_cache()
+    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16], elem_tol=None, what="paged decode > 4 GiB")
 
 
 def test_paged_decode_fp8_value_codes_exact(backend):
