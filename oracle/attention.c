@@ -106,7 +106,8 @@ int or_mha(const or_mha_config *config, const void *query, const void *key, cons
  * through its page table, then MultiHeadAttention with seqQ = 1 (causal mask is
  * bottom-right aligned, so the one query sees every key).
  * Pools: [pages, page_size, kv_heads, head_dim]; table [batch, max_pages_per_seq].
- * bf16 caches follow the bf16 MHA path.  fp8-E4M3 caches have no reference
+ * bf16 and f16 caches follow the MHA path of their dtype (query and output in
+ * the same dtype).  fp8-E4M3 caches have no reference
  * counterpart (device/cpu/shape/page.go:213-378 stops at f32/f16/bf16): they are
  * dequantised to f32 as decode(byte) * scale[kv head] and run through the f32
  * MHA path with the bf16 query widened; the output is stored as bf16. */
@@ -116,7 +117,7 @@ int or_paged_decode(const void *query, const void *key_pages, const void *value_
                     int64_t num_heads, int64_t kv_heads, int64_t head_dim,
                     const float *k_scale, const float *v_scale, int kv_dtype,
                     void *output) {
-    if (kv_dtype != OR_BF16 && kv_dtype != OR_F8E4M3) return -6;
+    if (kv_dtype != OR_BF16 && kv_dtype != OR_F16 && kv_dtype != OR_F8E4M3) return -6;
     int64_t inner = kv_heads * head_dim;
     or_mha_config c = {num_heads, head_dim, 1, 0, 0.0f, kv_heads};
     for (int64_t b = 0; b < batch; ++b) {
@@ -125,7 +126,7 @@ int or_paged_decode(const void *query, const void *key_pages, const void *value_
         const int32_t *table = page_table + b * max_pages_per_seq;
         const uint16_t *q16 = (const uint16_t *)query + b * num_heads * head_dim;
         uint16_t *o16 = (uint16_t *)output + b * num_heads * head_dim;
-        if (kv_dtype == OR_BF16) {
+        if (kv_dtype == OR_BF16 || kv_dtype == OR_F16) {
             uint16_t *kb = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(ctx * inner));
             uint16_t *vb = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)(ctx * inner));
             for (int64_t r = 0; r < ctx; ++r) {
@@ -133,7 +134,7 @@ int or_paged_decode(const void *query, const void *key_pages, const void *value_
                 memcpy(kb + r * inner, (const uint16_t *)key_pages + slot * inner, sizeof(uint16_t) * inner);
                 memcpy(vb + r * inner, (const uint16_t *)value_pages + slot * inner, sizeof(uint16_t) * inner);
             }
-            or_mha(&c, q16, kb, vb, o16, 1, ctx, OR_BF16);
+            or_mha(&c, q16, kb, vb, o16, 1, ctx, kv_dtype);
             free(kb);
             free(vb);
         } else {

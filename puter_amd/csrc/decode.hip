@@ -309,8 +309,12 @@ template <int KV, int G, bool O32>
 __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     constexpr int D = 128, TW = 64;
     constexpr bool BF = KV == PUTER_BF16;
-    // per-wave 32-row tiles: K rows (256 bytes bf16, 128 fp8), then V rows widened
-    // to bf16 (256 bytes), then the o merge
+    constexpr bool H16 = KV == PUTER_F16;   // f16 pools, query and output
+    constexpr bool W16 = BF || H16;          // 16-bit K/V rows (else fp8)
+    using P8 = typename std::conditional<H16, f16x8_t, bf16x8_t>::type;   // MFMA operand
+    using PE = typename std::conditional<H16, _Float16, __bf16>::type;
+    // per-wave 32-row tiles: K rows (256 bytes 16-bit, 128 fp8), then V rows (fp8
+    // widened to bf16: 256 bytes), then the o merge
     __shared__ __attribute__((aligned(1024))) char k_lds[4][32 * 256];
     __shared__ float ml_lds[4][G][2];
 
@@ -324,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     const int64_t inner = a.kv_heads * D;
     const int ps = (int)a.page_size;
     const int64_t head_off = (int64_t)kvh * D;
-    constexpr int EB = BF ? 2 : 1;
+    constexpr int EB = W16 ? 2 : 1;
     const uint8_t *kpool = static_cast<const uint8_t *>(a.kp);
     const uint8_t *vpool = static_cast<const uint8_t *>(a.vp);
     float acc[8][4];   // lane (grp, l16 < G): O[head l16][16 mt + 4 grp + r] = acc[mt][r]
@@ -344,33 +348,33 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                 if (page >= 0 && page < a.num_pages) myrow = page * ps + (tok - pidx * ps);
             }
         }
-        // every K and V row of the wave's 64 tokens, 16 bytes per lane: bf16 rows
+        // every K and V row of the wave's 64 tokens, 16 bytes per lane: 16-bit rows
         // (256 bytes) as token 4k + grp, piece l16; fp8 rows (128 bytes) as token
         // 8k + g8, piece l8 (dead rows read pool row 0: masked below)
-        constexpr int NL = BF ? 16 : 8;   // row loads per lane and tensor
+        constexpr int NL = W16 ? 16 : 8;   // row loads per lane and tensor
         const int g8 = lane >> 3, l8 = lane & 7;
         uint4 kb[NL], vb[NL];
 #pragma unroll
         for (int k = 0; k < NL; ++k) {
-            const int row = max(__shfl(myrow, BF ? 4 * k + grp : 8 * k + g8, 64), 0);
+            const int row = max(__shfl(myrow, W16 ? 4 * k + grp : 8 * k + g8, 64), 0);
             if constexpr (O32) {   // pools under 4 GiB: 32-bit offsets from the pool base
-                const uint32_t off = (uint32_t)row * (uint32_t)(inner * EB) + (uint32_t)(head_off * EB) + 16u * (BF ? l16 : l8);
+                const uint32_t off = (uint32_t)row * (uint32_t)(inner * EB) + (uint32_t)(head_off * EB) + 16u * (W16 ? l16 : l8);
                 kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
                 vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
             } else {
-                const int64_t off = ((int64_t)row * inner + head_off) * EB + 16 * (BF ? l16 : l8);
+                const int64_t off = ((int64_t)row * inner + head_off) * EB + 16 * (W16 ? l16 : l8);
                 kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
                 vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
             }
         }
         // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero
-        bf16x8_t qb[4];
+        P8 qb[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             uint4 u = make_uint4(0, 0, 0, 0);
             if (l16 < G)
                 u = *reinterpret_cast<const uint4 *>(a.q + ((int64_t)b * a.heads + (int64_t)kvh * G + l16) * D + 32 * t + 8 * grp);
-            qb[t] = __builtin_bit_cast(bf16x8_t, u);
+            qb[t] = __builtin_bit_cast(P8, u);
         }
         const uint64_t live = __ballot(myrow >= 0);   // token t live iff bit t
         char *tile = k_lds[wave];
@@ -387,7 +391,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             if (half) __builtin_amdgcn_wave_barrier();   // the first half's tile reads are done
-            if constexpr (BF) {
+            if constexpr (W16) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const int r = 4 * k + grp;
@@ -408,14 +412,15 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     uint4 kv;
-                    if constexpr (BF) kv = *reinterpret_cast<const uint4 *>(tile + row * 256 + (((4 * t + grp) ^ l16) << 4));
+                    if constexpr (W16) kv = *reinterpret_cast<const uint4 *>(tile + row * 256 + (((4 * t + grp) ^ l16) << 4));
                     else kv = fp8x8_to_bf16(*reinterpret_cast<const uint2 *>(tile + row * 128 + (((4 * t + grp) ^ (2 * ((l16 >> 1) & 7))) << 3)));
-                    acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], acc_s, 0, 0, 0);
+                    if constexpr (H16) acc_s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(P8, kv), qb[t], acc_s, 0, 0, 0);
+                    else acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(P8, kv), qb[t], acc_s, 0, 0, 0);
                 }
                 s[2 * half + i] = acc_s;
             }
         }
-        const float c = a.scale * (BF ? 1.0f : a.ks[kvh]) * 1.4426950408889634f;
+        const float c = a.scale * (W16 ? 1.0f : a.ks[kvh]) * 1.4426950408889634f;
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -423,6 +428,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
             for (int r = 0; r < 4; ++r) {
                 float v = s[i][r];
                 if constexpr (BF) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
+                if constexpr (H16) v = (float)(_Float16)v;              // f16 dot, likewise (RNE)
                 s[i][r] = v * c;
             }
         if (!full) {
@@ -458,17 +464,18 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
         // 32 tokens per step.  The k order of both operands: slot j of lane group
         // grp is token 16 (j / 4) + 4 grp + j % 4 of the step, which is where the
         // score accumulator left this lane's p (head l16), so P^T needs no shuffle.
-        // P enters as bf16 hi + lo halves (two MFMAs), a 16-bit significand: the
-        // products keep f32-grade accuracy, as the reference's f32 weights do.
-        bf16x8_t ph[2], pl[2];
+        // P enters as hi + lo halves in the operand format (two MFMAs: a 16-bit
+        // significand for bf16, 22 for f16): the products keep f32-grade
+        // accuracy, as the reference's f32 weights do.
+        P8 ph[2], pl[2];
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float p = s[2 * st + (j >> 2)][j & 3];
-                const __bf16 hi = (__bf16)p;
+                const PE hi = (PE)p;
                 ph[st][j] = hi;
-                pl[st][j] = (__bf16)(p - (float)hi);
+                pl[st][j] = (PE)(p - (float)hi);
             }
         f32x4_t ot[8];
 #pragma unroll
@@ -486,7 +493,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             __builtin_amdgcn_wave_barrier();   // the tile's previous reads are done
-            if constexpr (BF) {
+            if constexpr (W16) {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const int kk = 8 * st + k, r = 4 * k + grp;
@@ -519,9 +526,14 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                 const char *p = tile + vr * 256 + unit * 8;
                 const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
                 const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 16 * 256));
-                const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[st], ot[mt], 0, 0, 0);
-                ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[st], ot[mt], 0, 0, 0);
+                const P8 va = __builtin_bit_cast(P8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                if constexpr (H16) {
+                    ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph[st], ot[mt], 0, 0, 0);
+                    ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[st], ot[mt], 0, 0, 0);
+                } else {
+                    ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[st], ot[mt], 0, 0, 0);
+                    ot[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[st], ot[mt], 0, 0, 0);
+                }
             }
         }
         // lane (grp, l16): O[head l16][16 mt + 4 grp + r] = ot[mt][r]
@@ -711,7 +723,8 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     if (num_heads % kv_heads != 0) return fail(PUTER_ERR_INVALID, "paged decode: heads not divisible by kv heads");
     const int64_t G = num_heads / kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return fail(PUTER_ERR_INVALID, "paged decode: group size %lld unsupported", (long long)G);
-    if (kv_dtype != PUTER_BF16 && kv_dtype != PUTER_F8E4M3) return fail(PUTER_ERR_INVALID, "paged decode: kv dtype %d unsupported", kv_dtype);
+    if (kv_dtype != PUTER_BF16 && kv_dtype != PUTER_F16 && kv_dtype != PUTER_F8E4M3)
+        return fail(PUTER_ERR_INVALID, "paged decode: kv dtype %d unsupported", kv_dtype);
     if (num_pages > 0 && (num_pages > 0x7FFFFFFF / page_size || max_pages_per_seq > 0x7FFFFFFF / page_size))
         return fail(PUTER_ERR_INVALID, "paged decode: pool rows (num_pages * page_size) must stay below 2^31");
     if (max_context <= 0 || max_context > max_pages_per_seq * page_size)
@@ -742,7 +755,7 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     const dim3 grid((unsigned)kv_heads, (unsigned)splits, (unsigned)batch);
     // pools under 4 GiB take 32-bit row offsets
     const bool o32 = (uint64_t)num_pages * (uint64_t)page_size * (uint64_t)kv_heads * (uint64_t)head_dim *
-                         (kv_dtype == PUTER_BF16 ? 2u : 1u) < ((uint64_t)1 << 32);
+                         (kv_dtype == PUTER_F8E4M3 ? 1u : 2u) < ((uint64_t)1 << 32);
 #define PUTER_DECODE_G(KV, O)                                                         \
     switch (G) {                                                                      \
     case 1: decode_block_kernel<KV, 1, O><<<grid, 256, 0, s>>>(a); break;             \
@@ -755,6 +768,7 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     else { PUTER_DECODE_G(KV, false) }                                                \
     decode_combine_kernel<KV><<<dim3((unsigned)num_heads, (unsigned)batch), 128, 0, s>>>(a);
     if (kv_dtype == PUTER_BF16) { PUTER_DECODE(PUTER_BF16) }
+    else if (kv_dtype == PUTER_F16) { PUTER_DECODE(PUTER_F16) }
     else { PUTER_DECODE(PUTER_F8E4M3) }
 #undef PUTER_DECODE
 #undef PUTER_DECODE_G

@@ -401,6 +401,12 @@ def test_scaled_dot_product_attention(backend, dt, sq, sk, d, vd, causal):
                      elem_tol=1e-3 if dt == O.F32 else None, what="sdpa")
 
 
+def out_dtype(kv_dt):
+    """Query and output format of a paged decode: the pool's for f16 / bf16
+    pools, bf16 for fp8 pools."""
+    return O.F16 if kv_dt == O.F16 else O.BF16
+
+
 def paged_case(seed, batch, ctx_lo, ctx_hi, ps, h, kvh, d, kv_dt):
     rng = np.random.default_rng(seed)
     ctx = rng.integers(ctx_lo, ctx_hi + 1, batch).astype(np.int32)
@@ -413,11 +419,11 @@ def paged_case(seed, batch, ctx_lo, ctx_hi, ps, h, kvh, d, kv_dt):
     for i in range(batch):
         table[i, :npages[i]] = perm[at:at + npages[i]]
         at += npages[i]
-    q = O.from_f32(seeded(seed + 1, (batch, h * d)), O.BF16)
+    q = O.from_f32(seeded(seed + 1, (batch, h * d)), out_dtype(kv_dt))
     kf = seeded(seed + 2, (total, ps, kvh, d))
     vf = seeded(seed + 3, (total, ps, kvh, d))
-    if kv_dt == O.BF16:
-        kp, vp, ks, vs = O.from_f32(kf, O.BF16), O.from_f32(vf, O.BF16), None, None
+    if kv_dt in (O.BF16, O.F16):
+        kp, vp, ks, vs = O.from_f32(kf, kv_dt), O.from_f32(vf, kv_dt), None, None
     else:
         ks = (np.abs(kf).reshape(-1, kvh, d).max(axis=(0, 2)) / 448.0).astype(np.float32)
         vs = (np.abs(vf).reshape(-1, kvh, d).max(axis=(0, 2)) / 448.0).astype(np.float32)
@@ -441,32 +447,32 @@ def run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt
     return to_host(out, np.uint16)
 
 
-@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F16, O.F8E4M3])
 @pytest.mark.parametrize("batch,lo,hi,ps", [(3, 1, 40, 16), (4, 500, 1300, 16), (2, 256, 256, 16)])
 def test_paged_decode(backend, kv_dt, batch, lo, hi, ps):
     h, kvh, d = 32, 8, 128
     ctx, table, total, q, kp, vp, ks, vs = paged_case(batch * 100 + lo, batch, lo, hi, ps, h, kvh, d, kv_dt)
     ref = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, kv_dt, ks, vs)
     out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
-    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
-                 elem_tol=None, what="paged decode")
+    od = out_dtype(kv_dt)
+    assert_close(O.to_f32(out, od), O.to_f32(ref, od), TOL[od], elem_tol=None, what="paged decode")
 
 
-@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F16, O.F8E4M3])
 def test_paged_decode_pool_beyond_4gib(backend, kv_dt):
     """Pools of more than 4 GiB take 64-bit row offsets (smaller ones 32-bit):
     sequences whose pages lie past the 4 GiB mark of both pools, checked
     against the oracle on a compact copy of those pages."""
     import torch
     h, kvh, d, ps = 32, 8, 128, 16
-    es = 2 if kv_dt == O.BF16 else 1
+    es = 1 if kv_dt == O.F8E4M3 else 2
     row_bytes = kvh * d * es
     pages = (1 << 32) // (ps * row_bytes) + 2048           # just past 4 GiB per pool
     ctx, table, total, q, kp, vp, ks, vs = paged_case(77, 2, 150, 400, ps, h, kvh, d, kv_dt)
     far = (pages - total + np.arange(total)).astype(np.int32)   # compact page i -> pool page far[i]
     big_table = far[table]
-    tdt = torch.int16 if kv_dt == O.BF16 else torch.uint8
-    npd = np.int16 if kv_dt == O.BF16 else np.uint8
+    tdt = torch.uint8 if kv_dt == O.F8E4M3 else torch.int16
+    npd = np.uint8 if kv_dt == O.F8E4M3 else np.int16
     kpool = torch.zeros((pages, ps, kvh, d), dtype=tdt, device="cuda")
     vpool = torch.zeros((pages, ps, kvh, d), dtype=tdt, device="cuda")
     idx = torch.from_numpy(far.astype(np.int64)).cuda()
@@ -476,7 +482,8 @@ def test_paged_decode_pool_beyond_4gib(backend, kv_dt):
     out = run_paged_decode(backend, q, kpool, vpool, big_table, ctx, ps, pages, h, kvh, d, kv_dt, ks, vs)
     del kpool, vpool
     torch.cuda.empty_cache()
-    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16], elem_tol=None, what="paged decode > 4 GiB")
+    od = out_dtype(kv_dt)
+    assert_close(O.to_f32(out, od), O.to_f32(ref, od), TOL[O.BF16], elem_tol=None, what="paged decode > 4 GiB")
 
 
 def test_paged_decode_fp8_value_codes_exact(backend):
@@ -504,7 +511,7 @@ def test_paged_decode_fp8_value_codes_exact(backend):
 
 
 # group sizes 1, 2, 8 and page sizes that do not divide the 32-token sub-chunks
-@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F16, O.F8E4M3])
 @pytest.mark.parametrize("h,kvh", [(8, 8), (8, 4), (16, 2)])
 @pytest.mark.parametrize("ps,lo,hi", [(1, 1, 70), (5, 30, 300), (32, 200, 700)])
 def test_paged_decode_groups_pages(backend, kv_dt, h, kvh, ps, lo, hi):
@@ -512,11 +519,12 @@ def test_paged_decode_groups_pages(backend, kv_dt, h, kvh, ps, lo, hi):
     ctx, table, total, q, kp, vp, ks, vs = paged_case(7000 + 31 * h + kvh + ps, batch, lo, hi, ps, h, kvh, d, kv_dt)
     ref = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, kv_dt, ks, vs)
     out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
-    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
+    od = out_dtype(kv_dt)
+    assert_close(O.to_f32(out, od), O.to_f32(ref, od), TOL[od],
                  elem_tol=None, what="paged decode G=%d ps=%d" % (h // kvh, ps))
 
 
-@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F16, O.F8E4M3])
 def test_paged_decode_bad_page_ids_are_masked(backend, kv_dt):
     """A token whose page id is outside [0, num_pages) is masked: the result
     equals attention over the same sequence with that page removed."""
@@ -534,7 +542,8 @@ def test_paged_decode_bad_page_ids_are_masked(backend, kv_dt):
         ref_ctx[i] = ctx[i] - ps
     ref = O.paged_decode(q, kp, vp, ref_table, ref_ctx, ps, h, kvh, d, kv_dt, ks, vs)
     out = run_paged_decode(backend, q, kp, vp, bad, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
-    assert_close(O.to_f32(out, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16],
+    od = out_dtype(kv_dt)
+    assert_close(O.to_f32(out, od), O.to_f32(ref, od), TOL[od],
                  elem_tol=None, what="paged decode, bad page ids")
 
 

@@ -451,20 +451,21 @@ def test_flash_matches_single_head_mha_and_rounds_bf16_dot():
     assert np.max(np.abs(got - ref)) < 1e-2 * np.max(np.abs(ref))
 
 
-def test_paged_decode_matches_gather_then_mha():
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+def test_paged_decode_matches_gather_then_mha(dt):
     rng = np.random.default_rng(3)
     ps, h, kvh, d = 4, 4, 2, 8
     pages = 10
-    kp = O.from_f32(seeded(1, (pages, ps, kvh, d)), O.BF16)
-    vp = O.from_f32(seeded(2, (pages, ps, kvh, d)), O.BF16)
+    kp = O.from_f32(seeded(1, (pages, ps, kvh, d)), dt)
+    vp = O.from_f32(seeded(2, (pages, ps, kvh, d)), dt)
     table = rng.permutation(pages)[:6].reshape(2, 3).astype(np.int32)
     ctx = np.array([9, 12], np.int32)
-    q = O.from_f32(seeded(3, (2, h * d)), O.BF16)
-    got = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, O.BF16)
+    q = O.from_f32(seeded(3, (2, h * d)), dt)
+    got = O.paged_decode(q, kp, vp, table, ctx, ps, h, kvh, d, dt)
     for b in range(2):
         kk = O.page_gather(kp.reshape(-1), table[b], ps, kvh * d, int(ctx[b]))
         vv = O.page_gather(vp.reshape(-1), table[b], ps, kvh * d, int(ctx[b]))
-        ref = O.mha(q[b:b + 1], kk, vv, h, d, causal=True, kv_heads=kvh, dtype=O.BF16)
+        ref = O.mha(q[b:b + 1], kk, vv, h, d, causal=True, kv_heads=kvh, dtype=dt)
         assert np.array_equal(got[b], ref[0])
 
 
