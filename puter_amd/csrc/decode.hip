@@ -1,36 +1,31 @@
-// Paged-KV decode attention (one query token per sequence, GQA), bf16 or
-// fp8-E4M3 KV with a per-kv-head fp32 scale.
+// Paged-KV decode attention (one query token per sequence, GQA): bf16 or f16
+// K/V, or fp8-E4M3 K/V with a per-kv-head fp32 scale.
 //
 // Reference path: KVPageGather of K and V through the sequence's page table
 // (execution/page_intrinsic.go:217-352, device/cpu/shape/page_generic.go:45-63)
 // followed by MultiHeadAttention with seqQ = 1 (bind_router.go:640-684,
 // device/cpu/attention/typed_compute.go:142-237).  The gather is fused: K/V
 // rows are read straight from the page pools (no materialised [ctx, Hkv*D]
-// copies), so HBM traffic is the KV bytes read once.
+// copies), so HBM traffic is the KV bytes read once.  MultiHeadAttention with
+// one query row (the reference's own decode step, after its gather) runs the
+// same kernels over the contiguous K/V rows.
 //
 // Split-K ("flash decoding"): grid = (kv head, 256-token split, sequence), the
 // kv head fastest so the blocks reading the 8 head slices of the same pages run
-// together.  The paged decode runs decode_block_kernel (four waves of 64 tokens
-// per split, every row load of a wave issued at once, the waves' partials
-// merged in LDS); one-row MultiHeadAttention runs decode_kernel (one wave per
-// split walking it in 32-token sub-chunks with an online softmax, the next
-// sub-chunk's K and V rows loaded while the current one is computed).
+// together; decode_block_kernel runs four waves of 64 tokens per split, every
+// row load of a wave issued at once, the waves' partials merged in LDS.
 //   loads: every load instruction reads whole KV rows (16 lanes x 16 bytes =
-//     one 256-byte bf16 row), which measured 17-25% faster than loading K in
+//     one 256-byte 16-bit row), which measured 17-25% faster than loading K in
 //     the MFMA operand layout (16 rows x 64 bytes per instruction) or copying
 //     it HBM -> LDS directly.
-//   scores: S^T[token, head] = K . Q^T with v_mfma_f32_16x16x32_bf16; K rows
-//     reach the operand layout through a wave-private LDS tile (swizzled, bank-
+//   scores: S^T[token, head] = K . Q^T with v_mfma_f32_16x16x32; K rows reach
+//     the operand layout through a wave-private LDS tile (swizzled, bank-
 //     conflict free), B = the G query heads of the kv group, zero-padded to 16
 //     columns; a lane then holds 8 scores of one head.
-//   values (decode_block_kernel): O^T[d, head] = V^T . P^T on the same MFMA,
-//     V rows (fp8 widened to bf16) through the wave's LDS tile and read back
-//     transposed by ds_read_b64_tr_b16, P as bf16 hi + lo halves; the VALU FMA
-//     form it replaced left the fp8 kernel VALU-bound (78% VALU busy).
-//   values (decode_kernel): O[head, d] += p[head, token] * V[token, d] on the
-//     VALU: lane owns 8 dims of every 4th token, reads the token's G
-//     probabilities from a wave-private LDS row, accumulates G x 8 sums, and
-//     the 4 token-group partials are summed by lane-row swaps.
+//   values: O^T[d, head] = V^T . P^T on the same MFMA, V rows (fp8 widened to
+//     bf16) through the wave's LDS tile and read back transposed by
+//     ds_read_b64_tr_b16, P as hi + lo halves; the VALU FMA form it replaced
+//     left the fp8 kernel VALU-bound (78% VALU busy).
 // Each split leaves one (m, l, o[D]) per query head; decode_combine_kernel
 // merges the splits by log-sum-exp.
 #include "attention.hpp"
@@ -40,7 +35,7 @@
 
 namespace puter {
 
-constexpr int kSplit = 256;  // tokens per split (one wave, 8 sub-chunks of 32)
+constexpr int kSplit = 256;  // tokens per split (one block: four waves of 64 tokens)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -76,235 +71,16 @@ __device__ __forceinline__ uint4 fp8x8_to_bf16(uint2 raw) {
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// 8 f16 values -> f32 with the hardware widening: exact, and a signalling NaN
-// comes out quiet, which no attention output can tell apart (any NaN in a live
-// row makes the output NaN either way)
-__device__ __forceinline__ void f16x8_to_f32(const uint4 &w, float (&v)[8]) {
-    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] & 0xFFFFu));
-        v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
-    }
-}
-
-// One wave per (kv head, 256-token split, sequence): the split is walked in
-// eight 32-token sub-chunks with an online softmax.  Once sub-chunk n's rows
-// have landed and its K rows are parked in LDS, sub-chunk n+1's K and V rows
-// are loaded (V into a second register set) while n is computed, so every wave
-// keeps a sub-chunk of loads in flight while it works; small registers and LDS
-// let 8 waves share a CU.  Every load instruction reads whole KV rows: lane
-// group grp takes token 4k + grp, lane l16 its 16-byte piece l16.  K rows then
-// pass through a wave-private LDS tile (piece p of row r stored at p ^ (r % 16))
-// to reach the MFMA operand layout, 16 rows x one piece per read, bank-conflict
-// free.  One-row MultiHeadAttention runs it over bf16 or f16 K/V (KV).
-template <int KV, int G, int SPLIT = kSplit>
-__global__ __launch_bounds__(64, G <= 4 ? 2 : 1) void decode_kernel(DecodeArgs a) {
-    constexpr int D = 128, SUB = 32, NSUB = SPLIT / SUB, NGRP = (SPLIT + 63) / 64;
-    static_assert(KV == PUTER_BF16 || KV == PUTER_F16, "16-bit K/V only");
-    constexpr bool BF = KV == PUTER_BF16;
-    constexpr bool H16 = KV == PUTER_F16;         // f16 K/V and query
-    constexpr int RB = 256;                       // KV row bytes
-    using VT = uint4;
-    __shared__ __attribute__((aligned(1024))) char k_lds[SUB * RB];
-    __shared__ float p_lds[SUB][G];               // probabilities [token][head]
-
-    const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
-    // (null ctx / table: every sequence holds max_context tokens in contiguous rows,
-    // sequence b's token t at row b * page_size + t - one-row MultiHeadAttention)
-    const int ctx = a.ctx ? (int)min((int64_t)a.ctx[b], a.max_context) : (int)a.max_context;
-    const int t0 = split * SPLIT;
-    if (t0 >= ctx) return;
-    const int lane = threadIdx.x, l16 = lane & 15, grp = lane >> 4;
-    const int nsub = min(NSUB, (ctx - t0 + SUB - 1) / SUB);
-    const int64_t inner = a.kv_heads * D;
-    const int ps = (int)a.page_size;
-    const int32_t *table = a.table ? a.table + (int64_t)b * a.max_pages : nullptr;
-    const int64_t head_off = (int64_t)kvh * D;
-    const uint8_t *kpool = static_cast<const uint8_t *>(a.kp);
-    const uint8_t *vpool = static_cast<const uint8_t *>(a.vp);
-    constexpr int EB = 2;
-    // byte offset of this lane's piece of pool row `row`
-    auto piece = [&](int row) -> int64_t { return ((int64_t)row * inner + head_off) * EB + (int64_t)sizeof(VT) * l16; };
-
-    // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero
-    bf16x8_t qb[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        uint4 u = make_uint4(0, 0, 0, 0);
-        if (l16 < G)
-            u = *reinterpret_cast<const uint4 *>(a.q + ((int64_t)b * a.heads + (int64_t)kvh * G + l16) * D + 32 * t + 8 * grp);
-        qb[t] = __builtin_bit_cast(bf16x8_t, u);
-    }
-    // pool rows of the lane's tokens t0 + 64m + lane (-1: past the context or a
-    // bad page id); sub-chunk n holds tokens 32(n%2) .. +31 of group m = n/2
-    int myrow[NGRP];
-#pragma unroll
-    for (int n = 0; n < NGRP; ++n) {
-        myrow[n] = -1;
-        const int tok = t0 + 64 * n + lane;
-        if (tok < ctx) {
-            const int pidx = tok / ps;
-            const int32_t page = table ? table[pidx] : b * (int)a.max_pages + pidx;
-            if (page >= 0 && page < a.num_pages) myrow[n] = page * ps + (tok - pidx * ps);
-        }
-    }
-
-    VT kbuf[8], vbuf[2][8];   // rows of tokens 4k + grp of a sub-chunk, piece l16
-    // issue sub-chunk n's K and V row loads (dead rows, including whole
-    // sub-chunks past the context, read pool row 0, an L2 hit: their scores
-    // are masked and their V rows zeroed; the launcher never runs this kernel
-    // on an empty pool)
-    auto issue = [&](int n, VT (&kb)[8], VT (&vb)[8]) __attribute__((always_inline)) {
-        const int src = myrow[n >> 1], base = 32 * (n & 1);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int64_t off = piece(max(__shfl(src, base + 4 * k + grp, 64), 0));
-            kb[k] = ld_stream(reinterpret_cast<const uint4 *>(kpool + off));
-            vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
-        }
-    };
-
-    const float c = a.scale * 1.4426950408889634f;
-    float m_run = -INFINITY, l_run = 0.0f;   // head l16's running max (log2 domain) and sum
-    float acc[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
-
-    // sub-chunk n: wait for its rows, move its K rows into the LDS tile (which
-    // frees the K registers), issue sub-chunk n+1, then compute n
-    issue(0, kbuf, vbuf[0]);
-#pragma unroll
-    for (int n = 0; n < NSUB; ++n) {
-        if (n >= nsub) break;
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): sub-chunk n's loads have landed
-        VT (&vc)[8] = vbuf[n & 1];
-        // K rows -> LDS tile (row r = 4k + grp, piece l16 at l16 ^ swizzle(r))
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int r = 4 * k + grp;
-            *reinterpret_cast<uint4 *>(k_lds + r * 256 + ((l16 ^ (r & 15)) << 4)) = kbuf[k];
-        }
-        if (n + 1 < NSUB) issue(n + 1, kbuf, vbuf[(n + 1) & 1]);
-        __builtin_amdgcn_wave_barrier();   // the tile is private to this wave; LDS ops run in order
-        // token t of the sub-chunk is live iff bit t
-        const uint64_t live = __ballot(myrow[n >> 1] >= 0) >> (32 * (n & 1));
-        const uint64_t liveg = live >> (4 * grp);   // score (i, r): token 16i + 4grp + r
-        const uint64_t livev = live >> grp;         // V row k: token 4k + grp
-        // scores: A operand = K tile row 16i + l16, dims 32t + 8grp
-        f32x4_t s[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            s[i] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-            const int row = 16 * i + l16;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint4 kv = *reinterpret_cast<const uint4 *>(k_lds + row * 256 + (((4 * t + grp) ^ l16) << 4));
-                if constexpr (H16)
-                    s[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, kv),
-                                                                  __builtin_bit_cast(f16x8_t, qb[t]), s[i], 0, 0, 0);
-                else
-                    s[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv), qb[t], s[i], 0, 0, 0);
-            }
-        }
-        // lane's scores: head l16, tokens 16i + 4grp + r
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = s[i][r];
-                if constexpr (BF) v = round_reduction<PUTER_BF16>(v);  // bf16 dot, typed_compute.go:16-20
-                if constexpr (H16) v = (float)(_Float16)v;              // f16 dot, likewise (RNE)
-                v = ((liveg >> (16 * i + r)) & 1) ? v * c : -INFINITY;
-                s[i][r] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        const float mref = m_new == -INFINITY ? 0.0f : m_new;
-        float lsum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float p = s[i][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i][r] - mref);
-                lsum += p;
-                if (l16 < G) p_lds[16 * i + 4 * grp + r][l16] = p;
-            }
-        lsum += __shfl_xor(lsum, 16, 64);
-        lsum += __shfl_xor(lsum, 32, 64);
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-        __builtin_amdgcn_wave_barrier();
-        // rescale by head h's alpha (held by lane h), then accumulate p * V
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float ah = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(alpha), h));
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[h][j] *= ah;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t keep = ((livev >> (4 * k)) & 1) ? 0xFFFFFFFFu : 0u;  // dead rows: exact zeros
-            float v[8];
-            uint4 w = vc[k];
-            w.x &= keep; w.y &= keep; w.z &= keep; w.w &= keep;
-            if constexpr (H16) f16x8_to_f32(w, v);
-            else unpack_vec<PUTER_BF16>(w, v);
-            float p[G];
-#pragma unroll
-            for (int h = 0; h < G; ++h) p[h] = p_lds[4 * k + grp][h];
-#pragma unroll
-            for (int h = 0; h < G; ++h)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[h][j] = __builtin_fmaf(p[h], v[j], acc[h][j]);
-        }
-    }
-    // loads issued for a sub-chunk past the context are drained before exit
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    // sum the 4 token groups (16-lane rows): permlane16_swap pairs rows (0,1)
-    // and (2,3), permlane32_swap then pairs the halves; row grp writes head h's
-    // partial for the heads with h % 4 == grp
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float v = acc[h][j];
-            const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-            v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-            const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-            acc[h][j] = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
-        }
-    const int64_t slot0 = ((int64_t)b * a.heads + (int64_t)kvh * G) * a.max_splits + split;
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-        if ((h & 3) == grp) {
-            float4 *dst = reinterpret_cast<float4 *>(a.part_o + (slot0 + (int64_t)h * a.max_splits) * D + 8 * l16);
-            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-        }
-    if (grp == 0 && l16 < G) {
-        const int64_t slot = slot0 + (int64_t)l16 * a.max_splits;
-        a.part_ml[slot * 2] = m_run;   // log2-domain max of the scaled scores
-        a.part_ml[slot * 2 + 1] = l_run;
-    }
-}
-
 // Paged decode, block form: one 256-thread block per (kv head, 256-token split,
 // sequence); wave w takes the split's tokens 64w .. 64w + 63 and issues every K
 // and V row load of its 64 tokens at once (16-byte pieces: 32 KB of bf16 in
 // flight per wave), then computes them: scores on MFMA through a wave-private
 // LDS tile, the softmax of its 64 tokens against their own max, P.V on MFMA
 // through the same tile.  The four waves' (m, l, o) merge through LDS into the
-// split's partial, the same partial the wave-per-split kernel writes.  Measured
-// in one process on the configs[4] pool against the sub-chunk walk: bf16 +1%,
-// fp8 +4%; MFMA P.V with 16-byte fp8 row pieces then took fp8 from 144.6 to
-// 138.0 us (bf16 unchanged).
+// split's partial (m, l, o[D]) per query head.  Measured in one process on the
+// configs[4] pool against a one-wave-per-split walk over 32-token sub-chunks:
+// bf16 +1%, fp8 +4%; MFMA P.V with 16-byte fp8 row pieces then took fp8 from
+// 144.6 to 138.0 us (bf16 unchanged).
 template <int KV, int G, bool O32>
 __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     constexpr int D = 128, TW = 64;
@@ -654,13 +430,7 @@ bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *s
     if (!aligned16(m.q) || !aligned16(m.k) || !aligned16(m.v) || !aligned16(m.o)) return false;
     if (m.batch > 65535 || m.seq_k > 0x7FFFFFFF / std::max<int64_t>(m.batch, 1) || m.kv_heads > 0x7FFFFFFF)
         return false;
-    // 64-token splits (2 sub-chunks per wave) while 256-token splits would give fewer
-    // than 256 waves: a wave's sub-chunks run one after another, so few long splits
-    // are latency-bound (one sequence, 32 heads over 8: 4096 keys 24 -> 20 us; at
-    // 8192 keys the 256-token splits are already faster, 26 vs 29 us)
-    const bool short_splits = m.batch * m.kv_heads * splits_for(m.seq_k) < 256;
-    const int split = short_splits ? 64 : kSplit;
-    const int64_t splits = (m.seq_k + split - 1) / split;
+    const int64_t splits = splits_for(m.seq_k);
     if (splits > 65535) return false;
     const size_t need = (size_t)(m.batch * m.heads * splits) * (128 + 2) * sizeof(float);
     ScratchLease lease(need, s);
@@ -675,22 +445,22 @@ bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *s
                  m.kv_heads, splits, m.seq_k, m.scale};
     const dim3 grid((unsigned)m.kv_heads, (unsigned)splits, (unsigned)m.batch);
     const dim3 cgrid((unsigned)m.heads, (unsigned)m.batch);
-#define PUTER_ONE_ROW(KVD, SPL)                                                        \
+    const bool o32 = (uint64_t)m.batch * (uint64_t)m.seq_k * (uint64_t)m.kv_heads * 128u * 2u < ((uint64_t)1 << 32);
+#define PUTER_ONE_ROW_G(KVD, O)                                                        \
     switch (G) {                                                                       \
-    case 1: decode_kernel<KVD, 1, SPL><<<grid, 64, 0, s>>>(a); break;                  \
-    case 2: decode_kernel<KVD, 2, SPL><<<grid, 64, 0, s>>>(a); break;                  \
-    case 4: decode_kernel<KVD, 4, SPL><<<grid, 64, 0, s>>>(a); break;                  \
-    case 8: decode_kernel<KVD, 8, SPL><<<grid, 64, 0, s>>>(a); break;                  \
-    }                                                                                  \
-    decode_combine_kernel<KVD, SPL><<<cgrid, 128, 0, s>>>(a);
-    if (dtype == PUTER_BF16) {
-        if (short_splits) { PUTER_ONE_ROW(PUTER_BF16, 64) }
-        else { PUTER_ONE_ROW(PUTER_BF16, kSplit) }
-    } else {
-        if (short_splits) { PUTER_ONE_ROW(PUTER_F16, 64) }
-        else { PUTER_ONE_ROW(PUTER_F16, kSplit) }
+    case 1: decode_block_kernel<KVD, 1, O><<<grid, 256, 0, s>>>(a); break;             \
+    case 2: decode_block_kernel<KVD, 2, O><<<grid, 256, 0, s>>>(a); break;             \
+    case 4: decode_block_kernel<KVD, 4, O><<<grid, 256, 0, s>>>(a); break;             \
+    case 8: decode_block_kernel<KVD, 8, O><<<grid, 256, 0, s>>>(a); break;             \
     }
+#define PUTER_ONE_ROW(KVD)                                                             \
+    if (o32) { PUTER_ONE_ROW_G(KVD, true) }                                            \
+    else { PUTER_ONE_ROW_G(KVD, false) }                                               \
+    decode_combine_kernel<KVD><<<cgrid, 128, 0, s>>>(a);
+    if (dtype == PUTER_BF16) { PUTER_ONE_ROW(PUTER_BF16) }
+    else { PUTER_ONE_ROW(PUTER_F16) }
 #undef PUTER_ONE_ROW
+#undef PUTER_ONE_ROW_G
     const int rc = check_launch("mha one-row decode");
     const int fin = lease.finish();
     *status = rc ? rc : fin;
