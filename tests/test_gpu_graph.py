@@ -1,0 +1,134 @@
+"""GPU: one decode step captured in a HIP graph and replayed.
+
+The step is the paged-KV path of one generated token: KVPageWrite (bf16 pool) or
+KVPageWriteFP8 (fp8 pool) of the token's K and V rows at each sequence's next
+slot, PagedDecodeAttention over the grown contexts, and the fused
+GatedResidualRMSNorm of the attention output.  None of these entry points
+allocates, synchronises or issues a memset, so a caller can capture them.  Each
+replay runs with the step's inputs changed in place (new query, new K/V rows at
+the next slot, contexts one longer), with eager work and synchronisation between
+replays, and must equal the same calls made eagerly on a copy of the pools, bit
+for bit (output, hidden, attention output and both pools); the last replay's
+attention output is also checked against the oracle.
+
+Reference path: execution/page_intrinsic.go:135-352 (page write, gather),
+bind_router.go:640-684 (MultiHeadAttention), math_gated_residual_intrinsic.go."""
+import numpy as np
+import pytest
+
+import oracle as O
+import puter_amd
+from helpers import TOL, assert_close, seeded, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+def test_decode_step_graph_replays_match_eager(backend, kv_dt):
+    import torch
+
+    B, H, KV, D, PS, STEPS = 4, 16, 4, 128, 16, 3
+    inner, hid_dim = KV * D, H * D
+    rng = np.random.default_rng(900 + kv_dt)
+    ctx0 = rng.integers(100, 700, B).astype(np.int32)         # tokens already cached
+    npages = (ctx0 + STEPS + PS - 1) // PS                      # room for STEPS more
+    total = int(npages.sum())
+    perm = rng.permutation(total).astype(np.int32)
+    table = np.zeros((B, int(npages.max())), np.int32)
+    at = 0
+    for b in range(B):
+        table[b, :npages[b]] = perm[at:at + npages[b]]
+        at += npages[b]
+    max_ctx = int(ctx0.max()) + STEPS                           # fixed in the captured call
+
+    kf, vf = seeded(901, (total, PS, KV, D)), seeded(902, (total, PS, KV, D))
+    if kv_dt == O.BF16:
+        kp0, vp0, ks, vs = O.from_f32(kf, O.BF16), O.from_f32(vf, O.BF16), None, None
+    else:
+        ks = np.full(KV, 4.0 / 448.0, np.float32)
+        vs = np.full(KV, 4.0 / 448.0, np.float32)
+        kp0 = O.from_f32(kf / ks[0], O.F8E4M3)
+        vp0 = O.from_f32(vf / vs[0], O.F8E4M3)
+    kp, vp = to_dev(kp0), to_dev(vp0)
+    d_ks = None if ks is None else to_dev(ks)
+    d_vs = None if vs is None else to_dev(vs)
+    d_table = to_dev(table)
+    gamma = to_dev(O.from_f32(1.0 + 0.02 * seeded(903, (hid_dim,)), O.BF16))
+    mod = to_dev(O.from_f32(seeded(904, (1, 3 * hid_dim)), O.BF16))
+    ws_bytes = backend.PagedDecodeWorkspaceBytes(B, H, D, max_ctx)
+
+    def inputs(step):
+        pos = ctx0 + step                                       # the new token's index
+        ids = table[np.arange(B), pos // PS].astype(np.int32)
+        offs = (pos % PS).astype(np.int32)
+        return dict(q=O.from_f32(seeded(910 + step, (B, hid_dim)), O.BF16),
+                    knew=O.from_f32(seeded(920 + step, (B, inner)), O.BF16),
+                    vnew=O.from_f32(seeded(930 + step, (B, inner)), O.BF16),
+                    ids=ids, offs=offs, ctx=(pos + 1).astype(np.int32),
+                    x=O.from_f32(seeded(940 + step, (B, hid_dim)), O.BF16))
+
+    def buffers(inp):
+        return {k: to_dev(v) for k, v in inp.items()}
+
+    def outputs():
+        return dict(attn=torch.empty((B, hid_dim), dtype=torch.int16, device="cuda"),
+                    hid=torch.empty((B, hid_dim), dtype=torch.int16, device="cuda"),
+                    y=torch.empty((B, hid_dim), dtype=torch.int16, device="cuda"),
+                    ws=torch.empty(ws_bytes // 4, dtype=torch.float32, device="cuda"))
+
+    def step_calls(buf, out, k_pool, v_pool):
+        if kv_dt == O.BF16:
+            backend.KVPageWrite(k_pool, buf["knew"], buf["ids"], buf["offs"], k_pool, total, PS, inner,
+                                B, 0, O.BF16)
+            backend.KVPageWrite(v_pool, buf["vnew"], buf["ids"], buf["offs"], v_pool, total, PS, inner,
+                                B, 0, O.BF16)
+        else:
+            backend.KVPageWriteFP8(k_pool, buf["knew"], buf["ids"], buf["offs"], total, PS, KV, D, B, 0,
+                                   d_ks, O.BF16)
+            backend.KVPageWriteFP8(v_pool, buf["vnew"], buf["ids"], buf["offs"], total, PS, KV, D, B, 0,
+                                   d_vs, O.BF16)
+        backend.PagedDecodeAttention(buf["q"], k_pool, v_pool, d_table, buf["ctx"], B, table.shape[1], PS,
+                                     total, H, KV, D, max_ctx, d_ks, d_vs, kv_dt, out["attn"], out["ws"],
+                                     ws_bytes)
+        backend.GatedResidualRMSNorm(puter_amd.RMSNormConfig(1e-5), buf["x"], out["attn"], mod, gamma,
+                                     out["hid"], out["y"], B, hid_dim, B, 3 * hid_dim, 0, O.BF16)
+
+    # static buffers the graph reads and writes; one eager step first (it also
+    # creates the backend's status word outside the capture)
+    static = buffers(inputs(0))
+    sout = outputs()
+    step_calls(static, sout, kp, vp)
+    torch.cuda.synchronize()
+    backend.CheckStatus()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step_calls(static, sout, kp, vp)
+
+    for step in range(STEPS):
+        inp = inputs(step)
+        # eager reference on copies of the pools as they stand before this replay
+        k_ref, v_ref = kp.clone(), vp.clone()
+        eout = outputs()
+        step_calls(buffers(inp), eout, k_ref, v_ref)
+        torch.cuda.synchronize()
+        # new inputs into the graph's static buffers, then replay
+        for k, v in buffers(inp).items():
+            static[k].copy_(v)
+        graph.replay()
+        torch.cuda.synchronize()
+        backend.CheckStatus()
+        for name in ("attn", "hid", "y"):
+            assert torch.equal(sout[name], eout[name]), f"replay {step}: {name} differs from the eager step"
+        assert torch.equal(kp, k_ref) and torch.equal(vp, v_ref), f"replay {step}: pools differ"
+        # some unrelated eager work between replays
+        (torch.randn(1 << 20, device="cuda") * 2).sum().item()
+
+    # the last replay against the oracle (pools as the graph left them)
+    kh = to_host(kp, np.uint16 if kv_dt == O.BF16 else np.uint8)
+    vh = to_host(vp, np.uint16 if kv_dt == O.BF16 else np.uint8)
+    last = inputs(STEPS - 1)
+    ref = O.paged_decode(last["q"], kh.reshape(total, PS, KV, D), vh.reshape(total, PS, KV, D), table,
+                         last["ctx"], PS, H, KV, D, kv_dt, ks, vs)
+    got = to_host(sout["attn"], np.uint16)
+    assert_close(O.to_f32(got, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16], elem_tol=None,
+                 what="graph-replayed paged decode")
