@@ -49,6 +49,26 @@ class Timer:
         e.synchronize()
         return s.elapsed_time(e) / iters  # ms
 
+    def graph(self, fn, launches, reps=3):
+        """ms per launch of fn, with `launches` calls captured in one HIP graph and
+        the graph replayed: no host submission inside the timed region, so short
+        kernels are timed by the device, not by the host's launch rate."""
+        t = self.torch
+        g = t.cuda.CUDAGraph()
+        with t.cuda.graph(g):
+            for _ in range(launches):
+                fn()
+        g.replay()
+        t.cuda.synchronize()
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            g.replay()
+        e.record()
+        e.synchronize()
+        del g
+        return s.elapsed_time(e) / (reps * launches)
+
 
 class NormPool:
     """residual / branch / hidden / normed pools of n bf16 elements for the norm
@@ -111,11 +131,12 @@ def norm_sweep(torch, be, puter, steps, warmup):
         step()
     torch.cuda.synchronize()
     ms = timer.time(step, steps)
-    # per-shape figures and the dominant kernel, timed live with events
+    # per-shape figures (20 launches, each on the next pool window, captured in a
+    # HIP graph and replayed) and the dominant kernel, timed live with events
     per = {}
     for r, h, kind, fn in launches:
         fn()
-        t = timer.time(fn, 20)
+        t = timer.graph(fn, 20)
         per[f"{kind}_{r}x{h}"] = round(8 * r * h / (t * 1e-3) / 1e9, 1)
     dom = [x for x in launches if x[0] == rmax and x[1] == hmax and x[2] == "rms"][0]
     dom_ms = timer.time(dom[3], 50)
