@@ -442,7 +442,22 @@ def block_bf16(torch, be, puter):
         be.Matmul(y, o, W[3], S, HID, HID, puter.BF16)
 
     t = Timer(torch).time(chain, 50, warmup=3)
-    return {"block_bf16_us": round(t * 1e3, 1)}
+
+    # the same chain captured in a HIP graph (Matmul through the allocation-free
+    # entry point) and replayed: the block's device latency without host submission
+    def chain_graph():
+        be.RMSNorm(ncfg, x, g, h, S, HID, puter.BF16)
+        be.MatmulNoAlloc(q, h, W[0], S, HID, HID, puter.BF16)
+        be.MatmulNoAlloc(k, h, W[1], S, HID, HID, puter.BF16)
+        be.MatmulNoAlloc(v, h, W[2], S, HID, HID, puter.BF16)
+        be.RoPE(rcfg, q, q, S, H, D, puter.BF16)
+        be.RoPE(rcfg, k, k, S, H, D, puter.BF16)
+        be.MultiHeadAttention(mcfg, q, k, v, o, S, S, puter.BF16)
+        be.MatmulNoAlloc(y, o, W[3], S, HID, HID, puter.BF16)
+    chain_graph()
+    torch.cuda.synchronize()
+    tg = Timer(torch).graph(chain_graph, 1, reps=50)
+    return {"block_bf16_us": round(t * 1e3, 1), "block_bf16_graph_us": round(tg * 1e3, 1)}
 
 
 def block_f32(torch, be, puter):
@@ -490,6 +505,20 @@ def block_f32(torch, be, puter):
     torch.cuda.synchronize()
     got = y.cpu().numpy().reshape(S, HID)
     t = Timer(torch).time(gpu_chain, 50)
+
+    def graph_chain():   # captured in a HIP graph; Matmul through the allocation-free entry point
+        be.RMSNorm(ncfg, xd, gd, h, S, HID, puter.F32)
+        be.MatmulNoAlloc(q, h, wd[0], S, HID, HID, puter.F32)
+        be.MatmulNoAlloc(k, h, wd[1], S, HID, HID, puter.F32)
+        be.MatmulNoAlloc(v, h, wd[2], S, HID, HID, puter.F32)
+        be.RoPE(rcfg, q, q, S, H, D, puter.F32)
+        be.RoPE(rcfg, k, k, S, H, D, puter.F32)
+        be.MultiHeadAttention(mcfg, q, k, v, o, S, S, puter.F32)
+        be.MatmulNoAlloc(y, o, wd[3], S, HID, HID, puter.F32)
+    graph_chain()
+    torch.cuda.synchronize()
+    tg = Timer(torch).graph(graph_chain, 1, reps=50)
+    got_graph = y.cpu().numpy().reshape(S, HID)
     O.set_threads(1)
     ref = host_chain()
     reps, t0 = 0, time.perf_counter()
@@ -500,6 +529,7 @@ def block_f32(torch, be, puter):
     err = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
     flops = 4 * 2 * S * HID * HID + 4 * H * D * S * (S + 1) / 2
     return {"block_f32_us": round(t * 1e3, 1), "block_f32_GFLOPs": round(flops / (t * 1e-3) / 1e9, 1),
+            "block_f32_graph_us": round(tg * 1e3, 1), "block_f32_graph_equals_eager": bool(np.array_equal(got_graph, got)),
             "block_f32_normwise_err": err, "block_f32_cpu_us": round(cpu_ms * 1e3, 1),
             "block_f32_cpu_cores": 1}
 

@@ -7,8 +7,9 @@
 //
 // This file holds the general kernel (one block per (batch, head, query row),
 // online softmax over 256-key chunks staged in LDS, f32 accumulation) and the
-// dispatch: bf16 causal/non-causal prefill with D in {64, 128} and no
-// window/ALiBi goes to the MFMA flash kernel (prefill.hip).
+// dispatch: one query row in bf16 / f16 at head dim 128 goes to the split-K
+// decode kernels (decode.hip); bf16 / f16 causal or non-causal prefill at head
+// dim 128 with no window / ALiBi to the MFMA flash kernel (prefill.hip).
 #include "attention.hpp"
 
 namespace puter {
