@@ -510,9 +510,11 @@ def test_paged_decode_fp8_value_codes_exact(backend):
     assert np.array_equal(got[~nan], want[~nan])   # -0 sums to +0, as the reference's 0 + 1 * v does
 
 
-# group sizes 1, 2, 8 and page sizes that do not divide the 32-token sub-chunks
+# group sizes 1, 2, 4, 8; kv head counts 1, 2, 3, 4, 8 (the XCD grouping of kv heads
+# falls back to smaller groups, down to one, when it does not divide them); page
+# sizes that do not divide a wave's 64 tokens
 @pytest.mark.parametrize("kv_dt", [O.BF16, O.F16, O.F8E4M3])
-@pytest.mark.parametrize("h,kvh", [(8, 8), (8, 4), (16, 2)])
+@pytest.mark.parametrize("h,kvh", [(8, 8), (8, 4), (16, 2), (4, 1), (6, 3)])
 @pytest.mark.parametrize("ps,lo,hi", [(1, 1, 70), (5, 30, 300), (32, 200, 700)])
 def test_paged_decode_groups_pages(backend, kv_dt, h, kvh, ps, lo, hi):
     d, batch = 128, 3
