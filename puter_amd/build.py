@@ -1,4 +1,5 @@
-"""Build the gfx950 HIP library puter_amd/libputer_hip.so from puter_amd/csrc.
+"""Build the gfx950 HIP library puter_amd/libputer_hip.so from puter_amd/csrc,
+and the C++ host library puter_amd/libputer_host.so from puter_amd/host.
 
 Each .hip file is compiled ahead of time for gfx950 only (no JIT, no CUDA
 headers) into an object under puter_amd/_build/, then linked into one shared
@@ -46,6 +47,30 @@ def _compile(src: str) -> str:
     return obj
 
 
+HOST_SOURCES = ["host/backend.cpp", "host/kernels.cpp"]
+HOST_LIBRARY = os.path.join(HERE, "libputer_host.so")
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
+              "-I" + os.path.join(ROOT, "include"), "-I" + os.path.join(HERE, "host")]
+
+
+def build_host(verbose: bool = False) -> str:
+    """The C++ host side (puter_amd/host: the device.Backend methods, hooks,
+    workspace slots and kernel registry over the C ABI) into
+    puter_amd/libputer_host.so, linked against libputer_hip.so."""
+    tmp = HOST_LIBRARY + ".tmp"
+    cmd = ["g++", *HOST_FLAGS, *[os.path.join(HERE, s) for s in HOST_SOURCES], "-o", tmp,
+           "-L" + HERE, "-lputer_hip", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed for the host library:\n{r.stdout}\n{r.stderr}")
+    if r.stderr.strip():
+        sys.stderr.write(r.stderr)
+    os.replace(tmp, HOST_LIBRARY)
+    return HOST_LIBRARY
+
+
 def build(jobs: int = 8, verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     sources = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
@@ -57,6 +82,7 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIBRARY)
+    build_host(verbose)
     return LIBRARY
 
 
