@@ -362,6 +362,161 @@ CASE(workspace_slots_stay_on_device) {
     v16.Close();
 }
 
+CASE(adaptive_and_modulated_norms_f32) {
+    // AdaptiveRMSNorm: y = x inv (1 + scale) + shift; ModulatedLayerNorm with set 1
+    // (shift at 3H, scale at 3H + H): device/cpu/layernorm/compute.go:387-433,513-570
+    const int64_t rows = 12, h = 256, rpb = 4, batches = rows / rpb;
+    const DType dt = DType::Float32;
+    auto x = normal(141, rows * h, 0.2f, 1.5f);
+    auto amod = normal(142, batches * 2 * h, 0.0f, 0.1f), mmod = normal(143, batches * 6 * h, 0.0f, 0.1f);
+    Tensor dx = upload(x, {rows, h}, dt), da = upload(amod, {batches, 2 * h}, dt), dm = upload(mmod, {batches, 6 * h}, dt);
+    Tensor dy = be().AllocateTensor({rows, h}, dt), dz = be().AllocateTensor({rows, h}, dt);
+    RMSNormConfig rc;
+    rc.Epsilon = 1e-6;
+    be().AdaptiveRMSNorm(rc, dx.data, da.data, dy.data, rows, h, rpb, 2 * h, dt);
+    ModulatedLayerNormConfig mc;
+    mc.Epsilon = 1e-6;
+    mc.Set = 1;
+    be().ModulatedLayerNorm(mc, dx.data, dm.data, dz.data, rows, h, rpb, 6 * h, dt);
+    std::vector<float> ry(x.size()), rz(x.size());
+    EXPECT(or_adaptive_rmsnorm(x.data(), amod.data(), ry.data(), rows, h, rpb, 2 * h, 1e-6, 0) == 0, "oracle adaptive");
+    EXPECT(or_modulated_layernorm(x.data(), mmod.data(), rz.data(), rows, h, rpb, 6 * h, 1e-6, 1, 0) == 0,
+           "oracle modulated");
+    double e = normwise(download_f32(dy, dt), ry);
+    EXPECT(e <= 1e-5, "adaptive normwise %.3g", e);
+    e = normwise(download_f32(dz, dt), rz);
+    EXPECT(e <= 1e-5, "modulated normwise %.3g", e);
+}
+
+CASE(multi_axis_rope_and_rope_pairs) {
+    // 4 axes (text on axis 3) over a ragged 6-wide image grid after 8 text tokens
+    const int64_t b = 2, seq = 23, heads = 3, d = 16;
+    const DType dt = DType::BFloat16;
+    auto x = encode(normal(151, b * seq * heads * d), dt);
+    Tensor dx = upload(x, {b, seq, heads, d}, dt), dy = be().AllocateTensor({b, seq, heads, d}, dt);
+    MultiAxisRoPEConfig cfg;
+    cfg.BaseFreq = 1e4;
+    cfg.LatentSeqLen = 15;
+    cfg.LatentSide = 6;
+    cfg.AxisCount = 4;
+    cfg.AxisDim0 = 2;
+    cfg.AxisDim1 = 6;
+    cfg.AxisDim2 = 4;
+    cfg.AxisDim3 = 4;
+    be().MultiAxisRoPE(cfg, dx.data, dy.data, b, seq, heads, d, dt);
+    or_multi_axis_rope_config oc{1e4, 15, 6, 4, {2, 6, 4, 4}};
+    std::vector<uint8_t> ref(x.size());
+    EXPECT(or_multi_axis_rope(&oc, x.data(), ref.data(), b, seq, heads, d, static_cast<int>(dt)) == 0, "oracle");
+    double e = normwise(download_f32(dy, dt), decode(ref, dt, b * seq * heads * d));
+    EXPECT(e <= 1e-2, "multi-axis normwise %.3g", e);
+    // RoPEPairs (F32): (x cos - y sin, x sin + y cos) per pair, rope/f32_generic.go:3-11
+    const int64_t half = 1000;
+    auto in = normal(152, 2 * half), ang = normal(153, half, 0.0f, 2.0f);
+    std::vector<float> cs(half), sn(half);
+    for (int64_t i = 0; i < half; ++i) {
+        cs[i] = std::cos(ang[i]);
+        sn[i] = std::sin(ang[i]);
+    }
+    Tensor di = upload(in, {2 * half}, DType::Float32), dc = upload(cs, {half}, DType::Float32);
+    Tensor ds = upload(sn, {half}, DType::Float32), dout = be().AllocateTensor({2 * half}, DType::Float32);
+    be().RoPEPairs(dout.data, di.data, dc.data, ds.data, half, DType::Float32);
+    std::vector<float> pref(2 * half);
+    EXPECT(or_rope_pairs(pref.data(), in.data(), cs.data(), sn.data(), half) == 0, "oracle pairs");
+    e = normwise(download_f32(dout, DType::Float32), pref);
+    EXPECT(e <= 1e-5, "pairs normwise %.3g", e);
+}
+
+CASE(activations_packed_and_unary) {
+    // GeGLU packed rows [gate | up] (activation/gated.go) and Silu / Gelu in f32
+    const int64_t batch = 37, half = 640;
+    auto packed = normal(161, batch * 2 * half, 0.0f, 2.0f);
+    Tensor dp = upload(packed, {batch, 2 * half}, DType::Float32), dout = be().AllocateTensor({batch, half}, DType::Float32);
+    be().GeGLU(dout.data, dp.data, batch, half, DType::Float32);
+    std::vector<float> ref((size_t)(batch * half));
+    EXPECT(or_gated_packed(OR_GATE_GEGLU, ref.data(), packed.data(), batch, half, 0) == 0, "oracle geglu");
+    double e = normwise(download_f32(dout, DType::Float32), ref);
+    EXPECT(e <= 1e-5, "packed GeGLU normwise %.3g", e);
+    const int64_t n = 4099;
+    auto x = normal(162, n, 0.0f, 3.0f);
+    Tensor dx = upload(x, {n}, DType::Float32), dy = be().AllocateTensor({n}, DType::Float32);
+    be().Silu(dy.data, dx.data, n, DType::Float32);
+    std::vector<float> uref(n);
+    EXPECT(or_unary(OR_UNARY_SILU, uref.data(), x.data(), n, 0) == 0, "oracle silu");
+    e = normwise(download_f32(dy, DType::Float32), uref);
+    EXPECT(e <= 1e-5, "Silu normwise %.3g", e);
+    be().Gelu(dy.data, dx.data, n, DType::Float32);
+    EXPECT(or_unary(OR_UNARY_GELU, uref.data(), x.data(), n, 0) == 0, "oracle gelu");
+    e = normwise(download_f32(dy, DType::Float32), uref);
+    EXPECT(e <= 1e-5, "Gelu normwise %.3g", e);
+}
+
+CASE(scaled_dot_product_and_flash_attention) {
+    // single head, top-left causal mask, FastExp32 online softmax
+    // (device/cpu/attention/typed_compute.go:31-97)
+    for (DType dt : {DType::Float32, DType::BFloat16}) {
+        const int64_t sq = 70, sk = 90, d = 64, vd = 48;
+        const float sd = dt == DType::Float32 ? 0.25f : 0.125f;
+        auto q = encode(normal(171, sq * d, 0.0f, sd), dt), k = encode(normal(172, sk * d, 0.0f, sd), dt);
+        auto v = encode(normal(173, sk * vd), dt);
+        Tensor dq = upload(q, {sq, d}, dt), dk = upload(k, {sk, d}, dt), dv = upload(v, {sk, vd}, dt);
+        Tensor do1 = be().AllocateTensor({sq, vd}, dt), do2 = be().AllocateTensor({sq, vd}, dt);
+        FlashAttentionConfig cfg;
+        cfg.BlockSize = 64;
+        cfg.Causal = true;
+        be().ScaledDotProductAttention(cfg, dq.data, dk.data, dv.data, do1.data, sq, sk, d, vd, dt);
+        be().FlashAttention(cfg, dq.data, dk.data, dv.data, do2.data, sq, sk, d, vd, dt);
+        std::vector<uint8_t> ref((size_t)ByteCount(dt, sq * vd));
+        EXPECT(or_flash_attention(1, q.data(), k.data(), v.data(), ref.data(), sq, sk, d, vd, static_cast<int>(dt)) == 0,
+               "oracle");
+        const double tol = dt == DType::Float32 ? 1e-5 : 1e-2;
+        const auto want = decode(ref, dt, sq * vd);
+        double e = normwise(download_f32(do1, dt), want);
+        EXPECT(e <= tol, "%s SDPA normwise %.3g", Name(dt), e);
+        e = normwise(download_f32(do2, dt), want);
+        EXPECT(e <= tol, "%s Flash normwise %.3g", Name(dt), e);
+    }
+}
+
+CASE(kv_page_write_fp8_and_dequant4) {
+    // the quantising page write: byte = E4M3(value / scale[kv head]), bit-exact
+    const int64_t pages = 12, ps = 16, kvh = 4, hd = 128, inner = kvh * hd, rows = 30;
+    std::vector<uint8_t> pool((size_t)(pages * ps * inner));
+    for (size_t i = 0; i < pool.size(); ++i) pool[i] = (uint8_t)(i * 131 + 7);
+    std::vector<int32_t> ids(rows), offs(rows);
+    for (int64_t r = 0; r < rows; ++r) {
+        ids[r] = (int32_t)((r * 5 + 1) % pages);
+        offs[r] = (int32_t)((r * 3) % ps);
+    }
+    // distinct (page, slot) per row
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t q = 0; q < r; ++q) EXPECT(ids[r] != ids[q] || offs[r] != offs[q], "duplicate slot in the setup");
+    std::vector<float> scales = {0.5f, 0.03f, 1.0f, 0.2f};
+    auto vals = encode(normal(181, rows * inner, 0.0f, 30.0f), DType::BFloat16);
+    Tensor dpool = upload(pool, {pages, ps, inner}, DType::Float8E4M3), dv = upload(vals, {rows, inner}, DType::BFloat16);
+    Tensor di = upload(ids, {rows}, DType::Int32), doff = upload(offs, {rows}, DType::Int32);
+    Tensor dsc = upload(scales, {kvh}, DType::Float32);
+    be().KVPageWriteFP8(dpool.data, dv.data, di.data, doff.data, pages, ps, kvh, hd, rows, 0, dsc.data,
+                        DType::BFloat16);
+    std::vector<uint8_t> ref = pool;
+    EXPECT(or_page_write_fp8(ref.data(), vals.data(), ids.data(), offs.data(), pages, ps, kvh, hd, rows, 0,
+                             scales.data(), OR_BF16) == 0, "oracle");
+    EXPECT(download(dpool) == ref, "fp8 page write");
+    be().CheckStatus();
+    // Dequant4: packed signed nibbles (low first), (code - zero point) * scale
+    const int64_t n = 1001;
+    std::vector<uint8_t> packed((size_t)((n + 1) / 2));
+    for (size_t i = 0; i < packed.size(); ++i) packed[i] = (uint8_t)(i * 37 + 11);
+    Tensor dpk = upload(packed, {n}, DType::Int4), dout = be().AllocateTensor({n}, DType::Float32);
+    DequantInt4Config c4;
+    c4.Scale = 0.75f;
+    c4.ZeroPoint = -3;
+    be().Dequant4(dout.data, dpk.data, n, c4, DType::Float32, DType::Int4);
+    std::vector<float> dref(n);
+    EXPECT(or_dequant_int4(dref.data(), packed.data(), n, 0.75f, -3) == 0, "oracle dequant4");
+    const auto got = download(dout);
+    EXPECT(std::memcmp(got.data(), dref.data(), got.size()) == 0, "Dequant4");
+}
+
 int main(int argc, char **argv) {
     int count = 0;
     if (puter_hip_device_count(&count) != 0 || count < 1) {
