@@ -28,7 +28,7 @@ def build(verbose: bool = False) -> list:
     os.makedirs(BIN, exist_ok=True)
     out = []
     for name, oracle in PROGRAMS.items():
-        libs = ["-L" + os.path.join(ROOT, "puter_amd"), "-lputer_host", "-lputer_hip",
+        libs = ["-pthread", "-L" + os.path.join(ROOT, "puter_amd"), "-lputer_host", "-lputer_hip",
                 "-Wl,-rpath,$ORIGIN/../../../puter_amd", "-Wl,-rpath-link,/opt/rocm/lib"]
         if oracle:
             libs += ["-L" + os.path.join(ROOT, "oracle"), "-loracle", "-Wl,-rpath,$ORIGIN/../../../oracle",

@@ -5,7 +5,9 @@
 // gather, the gated residual's 16-bit output, SwiGLU and int8 quantisation;
 // normwise 1e-5 for f32 and 1e-2 for bf16 / fp8 otherwise.
 #include <algorithm>
+#include <atomic>
 #include <numeric>
+#include <thread>
 
 #include "backend.hpp"
 #include "check.hpp"
@@ -515,6 +517,77 @@ CASE(kv_page_write_fp8_and_dequant4) {
     EXPECT(or_dequant_int4(dref.data(), packed.data(), n, 0.75f, -3) == 0, "oracle dequant4");
     const auto got = download(dout);
     EXPECT(std::memcmp(got.data(), dref.data(), got.size()) == 0, "Dequant4");
+}
+
+CASE(host_threads_with_their_own_streams) {
+    // The shim must be thread-safe (one context, a stream per backend): four host
+    // threads, each with its own stream and Backend, run the split-K Matmul and
+    // one-row MultiHeadAttention (both lease the library's shared split-K scratch,
+    // ordered across streams by its completion event) and RMSNorm, 12 rounds each,
+    // all at once; every result equals the single-threaded one.  The scratch is
+    // grown to its final size by the single-threaded pass first, so the threads
+    // only share it.
+    const DType bf = DType::BFloat16;
+    const int64_t M = 64, K = 4096, N = 1024, H = 32, KVH = 8, D = 128, SK = 1500, R = 256, HID = 4096;
+    auto a = encode(normal(191, M * K), bf), b = encode(normal(192, K * N, 0.0f, 0.05f), bf);
+    auto q = encode(normal(193, H * D, 0.0f, 0.3f), bf), k = encode(normal(194, SK * KVH * D, 0.0f, 0.3f), bf);
+    auto v = encode(normal(195, SK * KVH * D), bf), x = encode(normal(196, R * HID), bf);
+    auto g = encode(normal(197, HID, 1.0f, 0.02f), bf);
+    Tensor da = upload(a, {M, K}, bf), db = upload(b, {K, N}, bf), dq = upload(q, {1, H * D}, bf);
+    Tensor dk = upload(k, {SK, KVH * D}, bf), dv = upload(v, {SK, KVH * D}, bf), dx = upload(x, {R, HID}, bf);
+    Tensor dg = upload(g, {HID}, bf);
+    MultiHeadAttentionConfig mha;
+    mha.NumHeads = H;
+    mha.HeadDim = D;
+    mha.Causal = true;
+    mha.KVHeadCount = KVH;
+    RMSNormConfig rc;
+    rc.Epsilon = 1e-5;
+    Tensor rmm = be().AllocateTensor({M, N}, bf), rat = be().AllocateTensor({1, H * D}, bf), rno = be().AllocateTensor({R, HID}, bf);
+    be().Matmul(rmm.data, da.data, db.data, M, K, N, bf);
+    be().MultiHeadAttention(mha, dq.data, dk.data, dv.data, rat.data, 1, SK, bf);
+    be().RMSNorm(rc, dx.data, dg.data, rno.data, R, HID, bf);
+    const auto want_mm = download(rmm), want_at = download(rat), want_no = download(rno);
+    constexpr int T = 4, ROUNDS = 12;
+    std::atomic<int> failures{0};
+    std::vector<std::string> why(T);
+    std::vector<std::thread> threads;
+    for (int t = 0; t < T; ++t) {
+        threads.emplace_back([&, t] {
+            void *stream = nullptr;
+            try {
+                Check(puter_hip_stream_create(&stream));
+                Backend mine(stream);
+                Tensor omm = mine.AllocateTensor({M, N}, bf), oat = mine.AllocateTensor({1, H * D}, bf);
+                Tensor ono = mine.AllocateTensor({R, HID}, bf);
+                std::vector<uint8_t> got;
+                for (int round = 0; round < ROUNDS; ++round) {
+                    mine.Matmul(omm.data, da.data, db.data, M, K, N, bf);
+                    mine.MultiHeadAttention(mha, dq.data, dk.data, dv.data, oat.data, 1, SK, bf);
+                    mine.RMSNorm(rc, dx.data, dg.data, ono.data, R, HID, bf);
+                    got.resize(want_mm.size());
+                    mine.Download(got.data(), omm.data, got.size());
+                    if (got != want_mm) throw std::runtime_error("Matmul differs in round " + std::to_string(round));
+                    got.resize(want_at.size());
+                    mine.Download(got.data(), oat.data, got.size());
+                    if (got != want_at) throw std::runtime_error("attention differs in round " + std::to_string(round));
+                    got.resize(want_no.size());
+                    mine.Download(got.data(), ono.data, got.size());
+                    if (got != want_no) throw std::runtime_error("RMSNorm differs in round " + std::to_string(round));
+                }
+            } catch (const std::exception &e) {
+                why[t] = e.what();
+                ++failures;
+            }
+            if (stream) {
+                puter_hip_stream_synchronize(stream);
+                puter_hip_stream_destroy(stream);
+            }
+        });
+    }
+    for (auto &th : threads) th.join();
+    for (int t = 0; t < T; ++t) EXPECT(why[t].empty(), "thread %d: %s", t, why[t].c_str());
+    EXPECT(failures == 0, "%d threads failed", failures.load());
 }
 
 int main(int argc, char **argv) {
