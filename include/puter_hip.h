@@ -3,7 +3,7 @@
  *
  * Every entry point mirrors one method of the reference's Go contract
  * (device/interface.go) or one optional execution hook, and is what a cgo
- * package `device/hip` binds (see INTEGRATION.md for the binding).  The
+ * package `device/hip` binds.  The
  * conventions follow the reference's call conventions:
  *
  *   - plain pointers (device addresses) and 64-bit sizes; no C++ or HIP types;

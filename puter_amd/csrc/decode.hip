@@ -79,7 +79,8 @@ __device__ __forceinline__ uint4 fp8x8_to_bf16(uint2 raw) {
 // LDS tile, the softmax of its 64 tokens against their own max, P.V on MFMA
 // through the same tile.  The four waves' (m, l, o) merge through LDS into the
 // split's partial (m, l, o[D]) per query head.  Measured in one process on the
-// configs[4] pool against a one-wave-per-split walk over 32-token sub-chunks:
+// 64-sequence decode pool (contexts U[512, 8192], page 16, 32 query heads over 8)
+// against a one-wave-per-split walk over 32-token sub-chunks:
 // bf16 +1%, fp8 +4%; MFMA P.V with 16-byte fp8 row pieces then took fp8 from
 // 144.6 to 138.0 us (bf16 unchanged).
 template <int KV, int G, bool O32>
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     // another, so for each token it reads gk adjacent head slices (1 KB: four
     // heads of 16-bit rows, eight of fp8) instead of one slice per XCD.  Against
     // one kv head per XCD: bf16 225.5 -> 220.4 us, fp8 136.4 -> 132.6 us on the
-    // configs[4] pool (one process); eight bf16 heads (2 KB) gave 223.7 us.
+    // 64-sequence decode pool (one process); eight bf16 heads (2 KB) gave 223.7 us.
     int kvh, split, b;
     {
         int gk = W16 ? 4 : 8;
