@@ -17,8 +17,9 @@ struct MhaArgs {
     int64_t shift;  // causal: key k is visible to query row q iff k <= q + shift
 };
 
-// MFMA bf16 flash prefill (prefill.hip).  Returns true and sets *status when
-// the shape is one it serves (bf16, head_dim 128, no window / ALiBi).
+// MFMA flash prefill (prefill.hip).  Returns true and sets *status when the
+// shape is one it serves (bf16 / f16, head_dim 128 or 64, no window / ALiBi;
+// head dim 64 only for more than one query row).
 bool launch_prefill_mfma(const MhaArgs &a, int dtype, hipStream_t s, int *status);
 // one query row per sequence (bf16 / f16, head_dim 128): the paged decode kernels
 bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *status);

@@ -14,9 +14,9 @@
 // normalizer, acc) one at a time, in key order, with the reference's exact
 // sequence of exponentials (FastExp32's error is ~1e-5 relative, so regrouping
 // the rescales would move f32 results by more than their tolerance); lanes own
-// the output dims.  bf16 with depth = valueDim = 128 runs on the MFMA
-// prefill kernel with one head and shift 0 (hardware exp2 in place of
-// FastExp32; the difference is far below bf16 resolution).
+// the output dims.  bf16 / f16 with depth = valueDim = 128 or 64 runs on the
+// MFMA prefill kernel with one head and shift 0 (hardware exp2 in place of
+// FastExp32; the difference is far below bf16 / f16 resolution).
 #include "attention.hpp"
 
 namespace puter {
@@ -107,8 +107,8 @@ static int run_flash(const puter_flash_config *config, const void *q, const void
     if (seq_q > 0x7FFFFFFF) return fail(PUTER_ERR_INVALID, "flash attention: grid too large");
     if (!q || !k || !v || !o) return fail(PUTER_ERR_NIL, "flash attention: nil buffer");
     const float scale = (float)(1.0 / sqrt((double)depth));
-    if ((dtype == PUTER_BF16 || dtype == PUTER_F16) && depth == 128 && value_dim == 128) {
-        MhaArgs m{q, k, v, o, 1, seq_q, seq_k, 1, 1, 128, config->causal ? 1 : 0, 0, 0.0f, scale, 0};
+    if ((dtype == PUTER_BF16 || dtype == PUTER_F16) && (depth == 128 || depth == 64) && value_dim == depth) {
+        MhaArgs m{q, k, v, o, 1, seq_q, seq_k, 1, 1, depth, config->causal ? 1 : 0, 0, 0.0f, scale, 0};
         int status = PUTER_OK;
         if (launch_prefill_mfma(m, dtype, s, &status)) return status;
     }

@@ -1,5 +1,6 @@
-// MFMA flash-attention prefill: bf16 or f16 Q/K/V (prefill_d128_kernel<dtype>),
-// f32 accumulation, output in the input format, head_dim 128, GQA, optional causal mask: key k is visible to query q when
+// MFMA flash-attention prefill: bf16 or f16 Q/K/V (prefill_kernel<dtype, head
+// dim>), f32 accumulation, output in the input format, head_dim 128 or 64, GQA,
+// optional causal mask: key k is visible to query q when
 // k <= q + shift.  MultiHeadAttention passes shift = seqK - seqQ (bottom-right
 // aligned, device/cpu/attention/typed_compute.go:166-168);
 // ScaledDotProductAttention passes 0 (typed_compute.go:60-62).
@@ -15,9 +16,10 @@
 // rows past the end arrive as zeros.  The wave index is read through
 // readfirstlane so all per-wave control flow is scalar.
 //
-// LDS layouts (one 16 KB tile each, 256-byte rows, no padding): K row r keeps
-// its 16-byte chunk c at position c ^ (r % 16) and V row r at c ^ 4*(r % 4);
-// both swizzles make the fragment reads below bank-conflict free.  The V^T
+// LDS layouts (one tile of 64 key rows each, no padding; 256-byte rows at head
+// dim 128, 128-byte rows at 64): K row r keeps its 16-byte chunk c at position
+// c ^ kswz(r) and V row r at c ^ vswz(r) (PfDim below); both swizzles make the
+// fragment reads below bank-conflict free.  The V^T
 // operand is read from the row-major V tile with ds_read_b64_tr_b16: within a
 // 16-lane group, result lane i gets element i%4 of the 8 bytes addressed by
 // lane 4j + i/4 as its element j, so lanes 4j..4j+3 pointing at four 4-dim
@@ -84,15 +86,35 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 namespace fa {
-constexpr int D = 128;        // head dim
 constexpr int BM = 128;       // queries per block (4 waves x 32)
 constexpr int BN = 64;        // keys per tile
-constexpr int TILE_BYTES = BN * D * 2;  // one K or V tile in LDS: 16 KB
 constexpr float RESCALE_SLACK = 8.0f;   // log2 headroom before O and l are rescaled
 constexpr float RESCALE_LIMIT = 256.0f; // 2^RESCALE_SLACK: the largest p allowed
 // buffer descriptor word 3 for raw (untyped, stride 0) dword access on gfx9
 constexpr int BUF_WORD3 = 0x00020000;
 }  // namespace fa
+
+// Per-head-dim layout of the K / V tiles (D = 128 or 64; 16-bit elements).
+// Rows are D * 2 bytes (16 or 8 chunks of 16 bytes).  K row r keeps chunk c at
+// c ^ kswz(r): with 256-byte rows kswz = r % 16, with 128-byte rows (two rows per
+// 64-bank line) kswz = (r / 2) % 8, so the 16 rows a fragment read touches fall
+// on distinct banks either way.  V row r keeps chunk c at c ^ vswz(r): 4 (r % 4)
+// for 256-byte rows, 4 ((r / 2) % 2) for 128-byte rows, so the four rows x 32
+// bytes of each transposing read (and the rows two apart that share a bank
+// line) do not collide.  Both swizzles are unchanged by row offsets of 8, 16
+// and 32, which the fragment reads add to a base row.
+template <int D> struct PfDim {
+    static_assert(D == 128 || D == 64, "head dim 128 or 64");
+    static constexpr int RB = D * 2;           // row bytes
+    static constexpr int NC = RB / 16;         // 16-byte chunks per row
+    static constexpr int TILE = fa::BN * RB;   // one K or V tile: 16 or 8 KB
+    static constexpr int KS = D / 16;          // S MFMA k-steps (16 dims each)
+    static constexpr int DB = D / 32;          // O^T blocks of 32 dims
+    static constexpr int RPI = 64 / NC;        // rows per copy instruction (64 lanes x 16 B)
+    static constexpr int NI = 16 / RPI;        // copy instructions per wave and tensor
+    static constexpr int kswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+    static constexpr int vswz(int r) { return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2); }
+};
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -107,8 +129,8 @@ struct PrefillArgs {
     float scale_log2;  // softmax scale * log2(e)
 };
 
-struct PrefillState {
-    f32x16 o[4];  // O^T accumulators: lane's query, dims 32d + 8*(r/4) + 4*(lane/32) + r%4
+template <int D> struct PrefillState {
+    f32x16 o[D / 32];  // O^T accumulators: lane's query, dims 32d + 8*(r/4) + 4*(lane/32) + r%4
     float m;      // reference max, scaled log2 domain (-inf: none yet)
     float l;      // this lane's half of the row sum
 };
@@ -126,13 +148,16 @@ __device__ __forceinline__ void wait_tile_copies() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's HBM -> LDS copies landed
 }
 
-// Copy K/V rows [kv0, kv0 + 64) of this head into LDS.  Wave w copies rows
-// 16*i + 4*w + lane/16 (i = 0..3): lane L fills chunk L%16 of its row with the
-// row's chunk (L%16) ^ swizzle(row) (kg / vg hold those byte offsets).
+// Copy K/V rows [kv0, kv0 + 64) of this head into LDS.  Each copy instruction
+// fills RPI consecutive rows (64 lanes x 16 bytes): wave w copies rows
+// 4 RPI i + RPI w + lane / NC (i < NI), lane L filling chunk L % NC of its row
+// with the row's chunk (L % NC) ^ swizzle(row) (kg / vg hold those byte offsets).
+template <int D>
 __device__ __forceinline__ void prefill_copy_tile(const PrefillArgs &a, const uint16_t *kbase,
-                                                  const uint16_t *vbase, int kv0, const int (&kg)[4],
-                                                  const int (&vg)[4], char *kdst, char *vdst, int wave) {
+                                                  const uint16_t *vbase, int kv0, const int *kg,
+                                                  const int *vg, char *kdst, char *vdst, int wave) {
     using namespace fa;
+    using T = PfDim<D>;
     const int rs2 = a.kv_heads * D * 2;  // K/V row stride in bytes
     const int rows = min(a.seq_k - kv0, BN);
     const int bytes = (rows - 1) * rs2 + D * 2;
@@ -142,11 +167,13 @@ __device__ __forceinline__ void prefill_copy_tile(const PrefillArgs &a, const ui
     const __amdgpu_buffer_rsrc_t vd =
         __builtin_amdgcn_make_buffer_rsrc((void *)(vbase + base), (short)0, bytes, BUF_WORD3);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(kd, (lds_void *)(kdst + (16 * i + 4 * wave) * 256), 16, kg[i], 0, 0, 0);
+    for (int i = 0; i < T::NI; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kd, (lds_void *)(kdst + (4 * T::RPI * i + T::RPI * wave) * T::RB), 16,
+                                                 kg[i], 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vd, (lds_void *)(vdst + (16 * i + 4 * wave) * 256), 16, vg[i], 0, 0, 0);
+    for (int i = 0; i < T::NI; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vd, (lds_void *)(vdst + (4 * T::RPI * i + T::RPI * wave) * T::RB), 16,
+                                                 vg[i], 0, 0, 0);
 }
 
 // One 64-key tile for this wave's 32 queries.  masked applies the causal and
@@ -159,21 +186,23 @@ __device__ __forceinline__ f32x16 pf_mfma(typename PfFormat<DT>::V8 a, typename 
     else return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int DT>
+template <int DT, int D>
 __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *ks, const char *vs,
-                                             const typename PfFormat<DT>::V8 (&qf)[8], PrefillState &st, int qi,
-                                             int kv0, const int (&ka)[8], const int (&va)[4], int g, bool masked) {
+                                             const typename PfFormat<DT>::V8 (&qf)[PfDim<D>::KS], PrefillState<D> &st,
+                                             int qi, int kv0, const int (&ka)[PfDim<D>::KS],
+                                             const int (&va)[PfDim<D>::DB], int g, bool masked) {
     using namespace fa;
+    using T = PfDim<D>;
     using V8 = typename PfFormat<DT>::V8;
     using E = typename PfFormat<DT>::E;
     // S^T chunks: keys kv0 + 32c + (8*(r/4) + 4g + r%4), query qi; two
     // independent accumulation chains interleaved
     f32x16 s[2] = {(f32x16){}, (f32x16){}};
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < T::KS; ++t)
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const V8 kf = *reinterpret_cast<const V8 *>(ks + c * 8192 + ka[t]);
+            const V8 kf = *reinterpret_cast<const V8 *>(ks + c * 32 * T::RB + ka[t]);
             s[c] = pf_mfma<DT>(kf, qf[t], s[c]);
         }
     if constexpr (DT == PUTER_F16) {
@@ -228,7 +257,7 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
             st.m = mnew;
             st.l *= alpha;
 #pragma unroll
-            for (int d = 0; d < 4; ++d)
+            for (int d = 0; d < D / 32; ++d)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) st.o[d][r] *= alpha;
         }
@@ -253,10 +282,10 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const char *p = vs + (32 * c + 16 * h) * 256 + va[d];
+            for (int d = 0; d < T::DB; ++d) {
+                const char *p = vs + (32 * c + 16 * h) * T::RB + va[d];
                 const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
-                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * 256));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * T::RB));
                 const V8 vf = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 st.o[d] = pf_mfma<DT>(vf, pf[c][h], st.o[d]);
             }
@@ -272,8 +301,8 @@ template <int DT> __device__ __forceinline__ float pf_score(float x) {
 // Online-softmax update for one 32-key chunk that needs the slow path (first
 // tile, or a score more than 2^8 above the reference): take the chunk max,
 // rescale O and l if the reference moves, and redo p against it.
-template <int DT>
-__device__ __forceinline__ float prefill_chunk_slow(const PrefillArgs &a, const f32x16 &s, PrefillState &st,
+template <int DT, int D>
+__device__ __forceinline__ float prefill_chunk_slow(const PrefillArgs &a, const f32x16 &s, PrefillState<D> &st,
                                                     typename PfFormat<DT>::V8 (&pf)[2]) {
     using namespace fa;
     using E = typename PfFormat<DT>::E;
@@ -287,7 +316,7 @@ __device__ __forceinline__ float prefill_chunk_slow(const PrefillArgs &a, const 
         st.m = mnew;
         st.l *= alpha;
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
+        for (int d = 0; d < D / 32; ++d)
 #pragma unroll
             for (int r = 0; r < 16; ++r) st.o[d][r] *= alpha;
     }
@@ -316,49 +345,54 @@ __device__ __forceinline__ float prefill_chunk_slow(const PrefillArgs &a, const 
 // chunk 0's contribution is in O and l, so a rescale there covers it.
 // sched_group_barrier fixes the interleave (the scheduler would otherwise
 // cluster the MFMAs and the VALU work apart).
-template <int DT>
+template <int DT, int D>
 __device__ __forceinline__ void prefill_step_pipelined(const PrefillArgs &a, const char *ks, const char *vs,
-                                                       const typename PfFormat<DT>::V8 (&qf)[8], PrefillState &st,
-                                                       const int (&ka)[8], const int (&va)[4]) {
+                                                       const typename PfFormat<DT>::V8 (&qf)[PfDim<D>::KS],
+                                                       PrefillState<D> &st, const int (&ka)[PfDim<D>::KS],
+                                                       const int (&va)[PfDim<D>::DB]) {
     using namespace fa;
+    using T = PfDim<D>;
     using V8 = typename PfFormat<DT>::V8;
     using E = typename PfFormat<DT>::E;
+    constexpr int KS = T::KS, NM = 2 * T::DB;   // S MFMAs per chunk, P.V MFMAs per chunk
+    constexpr int E2 = 16 / KS, E3 = 16 / NM;   // p values evaluated beside each MFMA (phases 2, 3)
+    constexpr int RA = KS < 4 ? KS : 4;         // K reads issued ahead of the first S MFMA
     f32x16 s0 = (f32x16){}, s1 = (f32x16){};
     V8 p0[2], p1[2];
     const float m = st.m, c = a.scale_log2;
     // phase 1 + 2
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < KS; ++t) {
         const V8 kf = *reinterpret_cast<const V8 *>(ks + ka[t]);
         s0 = pf_mfma<DT>(kf, qf[t], s0);
     }
     float ps0 = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const V8 kf = *reinterpret_cast<const V8 *>(ks + 8192 + ka[t]);
+    for (int t = 0; t < KS; ++t) {
+        const V8 kf = *reinterpret_cast<const V8 *>(ks + 32 * T::RB + ka[t]);
         s1 = pf_mfma<DT>(kf, qf[t], s1);
 #pragma unroll
-        for (int r = 2 * t; r < 2 * t + 2; ++r) {
+        for (int r = E2 * t; r < E2 * t + E2; ++r) {
             const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(pf_score<DT>(s0[r]), c, -m));
             ps0 += p;
             p0[r >> 3][r & 7] = (E)p;
         }
     }
-    // K fragment reads run 4 ahead of the MFMAs that use them (LDS latency
+    // K fragment reads run RA ahead of the MFMAs that use them (LDS latency
     // hidden behind the MFMAs in flight)
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);      // K reads c0 t0..3
+    __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);      // K reads c0 t0 ..
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < KS; ++t) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // S chunk 0 MFMA t
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K read (c0 t4..7, then c1 t0..3)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K read (c0, then c1)
     }
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < KS; ++t) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // S chunk 1 MFMA t
-        if (t < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // K read c1 t4..7
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // chunk 0 softmax share
+        if (t < KS - RA) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // remaining K reads of c1
+        __builtin_amdgcn_sched_group_barrier(0x002, 3 * E2, 0);  // chunk 0 softmax share
     }
-    if (__any(ps0 > RESCALE_LIMIT)) ps0 = prefill_chunk_slow<DT>(a, s0, st, p0);
+    if (__any(ps0 > RESCALE_LIMIT)) ps0 = prefill_chunk_slow<DT, D>(a, s0, st, p0);
     st.l += ps0;
     // phase 3: chunk 0's P.V with chunk 1's softmax between the MFMAs
     const float m1 = st.m;
@@ -366,15 +400,15 @@ __device__ __forceinline__ void prefill_step_pipelined(const PrefillArgs &a, con
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const char *p = vs + 16 * h * 256 + va[d];
+        for (int d = 0; d < T::DB; ++d) {
+            const char *p = vs + 16 * h * T::RB + va[d];
             const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
-            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * 256));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * T::RB));
             const V8 vf = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             st.o[d] = pf_mfma<DT>(vf, p0[h], st.o[d]);
-            const int r0 = 2 * (4 * h + d);
+            const int r0 = E3 * (T::DB * h + d);
 #pragma unroll
-            for (int r = r0; r < r0 + 2; ++r) {
+            for (int r = r0; r < r0 + E3; ++r) {
                 const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(pf_score<DT>(s1[r]), c, -m1));
                 ps1 += pv;
                 p1[r >> 3][r & 7] = (E)pv;
@@ -383,45 +417,46 @@ __device__ __forceinline__ void prefill_step_pipelined(const PrefillArgs &a, con
     // V^T fragment reads (two per MFMA) run two MFMAs ahead
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < NM; ++t) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // P.V MFMA (chunk 0)
-        if (t < 6) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // chunk 1 softmax share
+        if (t < NM - 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3 * E3, 0);  // chunk 1 softmax share
     }
-    if (__any(ps1 > RESCALE_LIMIT)) ps1 = prefill_chunk_slow<DT>(a, s1, st, p1);
+    if (__any(ps1 > RESCALE_LIMIT)) ps1 = prefill_chunk_slow<DT, D>(a, s1, st, p1);
     st.l += ps1;
     // phase 4: chunk 1's P.V
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const char *p = vs + (32 + 16 * h) * 256 + va[d];
+        for (int d = 0; d < T::DB; ++d) {
+            const char *p = vs + (32 + 16 * h) * T::RB + va[d];
             const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
-            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * 256));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p + 8 * T::RB));
             const V8 vf = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             st.o[d] = pf_mfma<DT>(vf, p1[h], st.o[d]);
         }
     __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < NM; ++t) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (t < 5) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        if (t < NM - 3) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
 }
 
-template <int DT>
-__global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
+template <int DT, int D>
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     using namespace fa;
+    using T = PfDim<D>;
     using V8 = typename PfFormat<DT>::V8;
     using V4 = typename PfFormat<DT>::V4;
     using E = typename PfFormat<DT>::E;
     // four separate arrays (not one indexed by parity) so the compiler can
     // tell the tile being copied from the tile being read and does not wait
     // for the copy before the reads
-    __shared__ __attribute__((aligned(1024))) char k0s[TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char k1s[TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char v0s[TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char v1s[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k0s[T::TILE];
+    __shared__ __attribute__((aligned(1024))) char k1s[T::TILE];
+    __shared__ __attribute__((aligned(1024))) char v0s[T::TILE];
+    __shared__ __attribute__((aligned(1024))) char v1s[T::TILE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -455,15 +490,15 @@ __global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
     const uint16_t *kbase = a.k + (int64_t)b * a.seq_k * krs + (int64_t)kvh * D;
     const uint16_t *vbase = a.v + (int64_t)b * a.seq_k * krs + (int64_t)kvh * D;
 
-    // this lane's query and its Q^T operand fragments (8 k-steps of 16 dims)
+    // this lane's query and its Q^T operand fragments (KS k-steps of 16 dims)
     const int qfirst = q0 + 32 * wave;
     const int qlast = min(qfirst + 31, a.seq_q - 1);
     const int qi = qfirst + l32;
-    V8 qf[8];
+    V8 qf[T::KS];
     {
         const int qload = min(qi, a.seq_q - 1);  // rows past the end compute garbage, never stored
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+        for (int t = 0; t < T::KS; ++t)
             qf[t] = __builtin_bit_cast(V8, *reinterpret_cast<const uint4 *>(qbase + (int64_t)qload * qrs + 16 * t + 8 * g));
     }
 
@@ -476,43 +511,41 @@ __global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
     nfree = min(nfree, ntiles);
 
     // byte offsets of this lane's tile copies (source side, swizzled) ...
-    int kg[4], vg[4];
+    int kg[T::NI], vg[T::NI];
     {
         const int rs2 = a.kv_heads * D * 2;
-        const int pos = lane & 15;
+        const int pos = lane % T::NC;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 16 * i + 4 * wave + (lane >> 4);
-            kg[i] = row * rs2 + ((pos ^ (row & 15)) << 4);
-            vg[i] = row * rs2 + ((pos ^ ((row & 3) << 2)) << 4);
+        for (int i = 0; i < T::NI; ++i) {
+            const int row = 4 * T::RPI * i + T::RPI * wave + lane / T::NC;
+            kg[i] = row * rs2 + ((pos ^ T::kswz(row)) << 4);
+            vg[i] = row * rs2 + ((pos ^ T::vswz(row)) << 4);
         }
     }
-    // ... and of its fragment reads: K row l32 (+32c), chunk (2t + g) ^ (l32 % 16);
+    // ... and of its fragment reads: K row l32 (+32c), chunk (2t + g) ^ kswz(l32);
     // V: lane group q = lane/16, i = lane%16 = 4j + m reads key row 4(q/2) + j,
-    // dims 16(q%2) + 4m .. +3 of dim block d: chunk (4d + 2(q%2) + m/2) ^ 4*(row%4), half m%2
-    int ka[8], va[4];
+    // dims 16(q%2) + 4m .. +3 of dim block d: chunk (4d + 2(q%2) + m/2) ^ vswz(row), half m%2
+    int ka[T::KS], va[T::DB];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) ka[t] = l32 * 256 + (((2 * t + g) ^ (l32 & 15)) << 4);
+    for (int t = 0; t < T::KS; ++t) ka[t] = l32 * T::RB + (((2 * t + g) ^ T::kswz(l32)) << 4);
     {
         const int q = lane >> 4, i = lane & 15, j = i >> 2, m = i & 3;
         const int row = 4 * (q >> 1) + j;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const int chunk = (4 * d + 2 * (q & 1) + (m >> 1)) ^ ((row & 3) << 2);
-            va[d] = row * 256 + (chunk << 4) + 8 * (m & 1);
+        for (int d = 0; d < T::DB; ++d) {
+            const int chunk = (4 * d + 2 * (q & 1) + (m >> 1)) ^ T::vswz(row);
+            va[d] = row * T::RB + (chunk << 4) + 8 * (m & 1);
         }
     }
-    PrefillState st;
+    PrefillState<D> st;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) st.o[d] = (f32x16){};
+    for (int d = 0; d < T::DB; ++d) st.o[d] = (f32x16){};
     st.m = -INFINITY;
     st.l = 0.0f;
 
-    if (ntiles > 0) prefill_copy_tile(a, kbase, vbase, 0, kg, vg, k0s, v0s, wave);
+    if (ntiles > 0) prefill_copy_tile<D>(a, kbase, vbase, 0, kg, vg, k0s, v0s, wave);
     wait_tile_copies();
     __syncthreads();
-    // one tile: copy the next tile into the other buffers, compute this one,
-    // then wait for the copy and meet at the barrier
     // One tile: copy the next tile into the other buffers, compute this one, then
     // wait for the copy and meet at the barrier.  The mask-free tiles [0, nfree)
     // come first and run in a loop of their own (two tiles per iteration so the
@@ -520,8 +553,8 @@ __global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
     // follow in a second loop, so the O accumulators never pass through a merge
     // of the two paths (which cost a register copy of O per tile).
     auto tile_free = [&](int it, const char *kc, const char *vc, char *kn, char *vn) __attribute__((always_inline)) {
-        if (it + 1 < ntiles) prefill_copy_tile(a, kbase, vbase, (it + 1) * BN, kg, vg, kn, vn, wave);
-        prefill_step_pipelined<DT>(a, kc, vc, qf, st, ka, va);
+        if (it + 1 < ntiles) prefill_copy_tile<D>(a, kbase, vbase, (it + 1) * BN, kg, vg, kn, vn, wave);
+        prefill_step_pipelined<DT, D>(a, kc, vc, qf, st, ka, va);
         wait_tile_copies();
         __syncthreads();
     };
@@ -537,10 +570,11 @@ __global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
     for (; it < ntiles; ++it) {
         const int kv0 = it * BN;
         const bool odd = it & 1;
-        if (it + 1 < ntiles) prefill_copy_tile(a, kbase, vbase, kv0 + BN, kg, vg, odd ? k0s : k1s, odd ? v0s : v1s, wave);
+        if (it + 1 < ntiles)
+            prefill_copy_tile<D>(a, kbase, vbase, kv0 + BN, kg, vg, odd ? k0s : k1s, odd ? v0s : v1s, wave);
         // waves whose queries all precede this tile skip it
         if (!a.causal || kv0 <= qlast + a.shift)
-            prefill_step<DT>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
+            prefill_step<DT, D>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
         wait_tile_copies();
         __syncthreads();
     }
@@ -551,7 +585,7 @@ __global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
     if (qi < a.seq_q) {
         uint16_t *orow = a.o + (int64_t)b * a.seq_q * qrs + (int64_t)qi * qrs + (int64_t)h * D;
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
+        for (int d = 0; d < T::DB; ++d)
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
                 V4 v;
@@ -563,7 +597,10 @@ __global__ __launch_bounds__(256, 2) void prefill_d128_kernel(PrefillArgs a) {
 }
 
 bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
-    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || m.dim != 128 || m.window > 0 || m.alibi != 0.0f) return false;
+    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || (m.dim != 128 && m.dim != 64) || m.window > 0 ||
+        m.alibi != 0.0f)
+        return false;
+    if (m.dim == 64 && m.seq_q == 1) return false;   // one query row: the general kernel (no 127 padding rows)
     if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF)
         return false;
     // 32-bit buffer offsets: one 64-row tile of K/V must span < 2^31 bytes
@@ -589,8 +626,13 @@ bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status
     a.scale_log2 = m.scale * 1.4426950408889634f;
     const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;
     if (blocks > 0x7FFFFFFF) return false;
-    if (dtype == PUTER_BF16) prefill_d128_kernel<PUTER_BF16><<<(unsigned)blocks, 256, 0, s>>>(a);
-    else prefill_d128_kernel<PUTER_F16><<<(unsigned)blocks, 256, 0, s>>>(a);
+    if (m.dim == 128) {
+        if (dtype == PUTER_BF16) prefill_kernel<PUTER_BF16, 128><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else prefill_kernel<PUTER_F16, 128><<<(unsigned)blocks, 256, 0, s>>>(a);
+    } else {
+        if (dtype == PUTER_BF16) prefill_kernel<PUTER_BF16, 64><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else prefill_kernel<PUTER_F16, 64><<<(unsigned)blocks, 256, 0, s>>>(a);
+    }
     *status = check_launch("prefill mfma");
     return true;
 }

@@ -202,10 +202,12 @@ CASE(kv_page_write_gather_and_status) {
 }
 
 CASE(multi_head_attention_bf16_prefill_and_one_row) {
+    // head dim 128 (prefill and one-row kernels) and 64 (the prefill kernel's other layout)
     const DType dt = DType::BFloat16;
-    struct Shape { int64_t sq, sk, h, kvh; bool causal; };
-    for (Shape s : {Shape{256, 256, 8, 2, true}, Shape{1, 700, 32, 8, true}, Shape{96, 160, 4, 4, false}}) {
-        const int64_t d = 128;
+    struct Shape { int64_t sq, sk, h, kvh, d; bool causal; };
+    for (Shape s : {Shape{256, 256, 8, 2, 128, true}, Shape{1, 700, 32, 8, 128, true},
+                    Shape{96, 160, 4, 4, 128, false}, Shape{300, 300, 8, 8, 64, true}}) {
+        const int64_t d = s.d;
         auto q = encode(normal(81, s.sq * s.h * d, 0.0f, 0.3f), dt);
         auto k = encode(normal(82, s.sk * s.kvh * d, 0.0f, 0.3f), dt), v = encode(normal(83, s.sk * s.kvh * d), dt);
         Tensor dq = upload(q, {s.sq, s.h * d}, dt), dk = upload(k, {s.sk, s.kvh * d}, dt), dv = upload(v, {s.sk, s.kvh * d}, dt);

@@ -358,9 +358,9 @@ def test_prefill_rows_agree_with_one_row_path_bf16(backend):
     (1, 96, 40, 4, 2, True),        # seqQ > seqK: leading queries see no key -> zeros
 ])
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
-def test_prefill_mfma_shapes(backend, dt, b, sq, sk, h, kvh, causal):
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_mfma_shapes(backend, dt, d, b, sq, sk, h, kvh, causal):
     import puter_amd
-    d = 128
     std = 1.0 / np.sqrt(d)
     q = encode(seeded(300 + sq, (b, sq, h * d), 0.0, std), dt)
     k = encode(seeded(301 + sk, (b, sk, kvh * d), 0.0, std), dt)
