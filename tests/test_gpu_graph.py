@@ -1,6 +1,10 @@
-"""GPU: one decode step captured in a HIP graph and replayed.
+"""GPU: the hot path captured in HIP graphs and replayed.
 
-The step is the paged-KV path of one generated token: KVPageWrite (bf16 pool) or
+A decode step (below) and a bf16 pre-norm transformer block (the last test) are
+each captured once and replayed with new inputs; every replay must equal the same
+calls made eagerly, bit for bit.
+
+The decode step is the paged-KV path of one generated token: KVPageWrite (bf16 pool) or
 KVPageWriteFP8 (fp8 pool) of the token's K and V rows at each sequence's next
 slot, PagedDecodeAttention over the grown contexts, and the fused
 GatedResidualRMSNorm of the attention output.  None of these entry points
@@ -132,3 +136,68 @@ def test_decode_step_graph_replays_match_eager(backend, kv_dt):
     got = to_host(sout["attn"], np.uint16)
     assert_close(O.to_f32(got, O.BF16), O.to_f32(ref, O.BF16), TOL[O.BF16], elem_tol=None,
                  what="graph-replayed paged decode")
+
+
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_prefill_block_graph_replays_match_eager(backend, head_dim):
+    """A bf16 pre-norm transformer block (RMSNorm, Q/K/V projections, RoPE on Q
+    and K, causal grouped-query MultiHeadAttention on the MFMA prefill kernel,
+    output projection, gated residual, SwiGLU MLP with its projections, and an
+    f32 cast of the result) captured once in a HIP graph and replayed three times
+    with new activations each time; every replay equals the eager calls bit for
+    bit.  Matmul goes through its allocation-free entry point."""
+    import torch
+
+    S, H, KVH, D = 256, 8, 2, head_dim
+    HID, KVD, FF = H * D, KVH * D, 2 * H * D
+    bf = O.BF16
+    w = {n: to_dev(O.from_f32(seeded(1000 + i, shape, 0.0, 0.02), bf))
+         for i, (n, shape) in enumerate([("wq", (HID, HID)), ("wk", (HID, KVD)), ("wv", (HID, KVD)),
+                                         ("wo", (HID, HID)), ("wg", (HID, FF)), ("wu", (HID, FF)),
+                                         ("wd", (FF, HID))])}
+    gamma = to_dev(O.from_f32(1.0 + 0.02 * seeded(1010, (HID,)), bf))
+    mod = to_dev(O.from_f32(seeded(1011, (1, 3 * HID)), bf))
+    rope = puter_amd.RoPEConfig(BaseFreq=10000.0)
+    mha = puter_amd.MultiHeadAttentionConfig(H, D, True, 0, 0.0, KVH)
+
+    def buffers():
+        e = lambda *shape: torch.empty(shape, dtype=torch.int16, device="cuda")  # noqa: E731
+        return dict(h=e(S, HID), q=e(S, HID), k=e(S, KVD), v=e(S, KVD), o=e(S, HID), a=e(S, HID),
+                    r=e(S, HID), g=e(S, FF), u=e(S, FF), f=e(S, FF), y=e(S, HID),
+                    y32=torch.empty((S, HID), dtype=torch.float32, device="cuda"))
+
+    def block(x, b):
+        be = backend
+        be.RMSNorm(puter_amd.RMSNormConfig(1e-6), x, gamma, b["h"], S, HID, bf)
+        be.MatmulNoAlloc(b["q"], b["h"], w["wq"], S, HID, HID, bf)
+        be.MatmulNoAlloc(b["k"], b["h"], w["wk"], S, HID, KVD, bf)
+        be.MatmulNoAlloc(b["v"], b["h"], w["wv"], S, HID, KVD, bf)
+        be.RoPE(rope, b["q"], b["q"], S, H, D, bf)
+        be.RoPE(rope, b["k"], b["k"], S, KVH, D, bf)
+        be.MultiHeadAttention(mha, b["q"], b["k"], b["v"], b["o"], S, S, bf)
+        be.MatmulNoAlloc(b["a"], b["o"], w["wo"], S, HID, HID, bf)
+        be.GatedResidual(x, b["a"], mod, b["r"], S, HID, S, 3 * HID, 0, bf)
+        be.MatmulNoAlloc(b["g"], b["r"], w["wg"], S, HID, FF, bf)
+        be.MatmulNoAlloc(b["u"], b["r"], w["wu"], S, HID, FF, bf)
+        be.SwiGLUTensors(b["f"], b["g"], b["u"], S * FF, bf)
+        be.MatmulNoAlloc(b["y"], b["f"], w["wd"], S, FF, HID, bf)
+        be.Cast(b["y32"], O.F32, b["y"], bf, S * HID)
+
+    x_static = to_dev(O.from_f32(seeded(1020, (S, HID)), bf))
+    out_static = buffers()
+    block(x_static, out_static)      # eager warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        block(x_static, out_static)
+    for step in range(3):
+        x = to_dev(O.from_f32(seeded(1030 + step, (S, HID)), bf))
+        ref = buffers()
+        block(x, ref)
+        torch.cuda.synchronize()
+        x_static.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        for name in ("h", "q", "k", "o", "r", "f", "y", "y32"):
+            assert torch.equal(out_static[name], ref[name]), f"replay {step}: {name} differs from the eager block"
+        (torch.randn(1 << 20, device="cuda") + 1).sum().item()   # eager work between replays
