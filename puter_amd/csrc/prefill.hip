@@ -3,7 +3,10 @@
 // optional causal mask: key k is visible to query q when
 // k <= q + shift.  MultiHeadAttention passes shift = seqK - seqQ (bottom-right
 // aligned, device/cpu/attention/typed_compute.go:166-168);
-// ScaledDotProductAttention passes 0 (typed_compute.go:60-62).
+// ScaledDotProductAttention passes 0 (typed_compute.go:60-62).  Optional
+// sliding window: key k is visible to query q only when q - k < window
+// (typed_compute.go:172); a block skips the key tiles below its first query's
+// window and masks those below its last query's.
 //
 // Work split: one 256-thread block (4 wave64s) per (128-query tile, head,
 // batch); wave w owns 32 queries; two blocks share a CU (2 waves per SIMD, so
@@ -126,6 +129,7 @@ struct PrefillArgs {
     int batch, seq_q, seq_k, heads, kv_heads, qtiles;
     int causal, xcd_map;
     int shift;         // causal: key k visible to query q iff k <= q + shift
+    int window;        // > 0: key k visible to query q only if k > q - window
     float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -215,14 +219,18 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
     }
     if (masked) {
         // key kv0 + 32c + 8(r/4) + 4g + r%4 is visible iff its offset past
-        // kv0 + 4g is <= lim (the query's last visible key, relative)
+        // kv0 + 4g lies in [lo, lim] (the query's first and last visible keys,
+        // relative; the first is the sliding window's lower edge)
         const int last = a.causal ? min(qi + a.shift, a.seq_k - 1) : a.seq_k - 1;
         const int lim = last - kv0 - 4 * g;
+        const int lo = (a.window > 0 ? qi - a.window + 1 : 0) - kv0 - 4 * g;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                s[c][r] = (32 * c + 8 * (r >> 2) + (r & 3)) > lim ? -INFINITY : s[c][r];
+            for (int r = 0; r < 16; ++r) {
+                const int off = 32 * c + 8 * (r >> 2) + (r & 3);
+                s[c][r] = (off > lim || off < lo) ? -INFINITY : s[c][r];
+            }
     }
     // Fast path: every lane already has a reference and p = exp2(s*c - m) is
     // evaluated without the tile max; since every p <= the row sum, a sum <= 2^8
@@ -502,13 +510,22 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             qf[t] = __builtin_bit_cast(V8, *reinterpret_cast<const uint4 *>(qbase + (int64_t)qload * qrs + 16 * t + 8 * g));
     }
 
-    // key tiles of the block: [0, ntiles); tiles [0, nfree) need no mask for any query of it
+    // key tiles of the block: [tlo, ntiles); tiles [tfree, nfree) need no mask for
+    // any query of it.  Without a window tlo = tfree = 0; with one, the tiles below
+    // the first query's window are skipped and those below the last query's window
+    // edge are masked.
     int kend = a.seq_k;
     if (a.causal) kend = min(kend, min(q0 + BM, a.seq_q) + a.shift);
     const int ntiles = kend > 0 ? (kend + BN - 1) / BN : 0;
     int nfree = a.seq_k / BN;
     if (a.causal) nfree = min(nfree, q0 + a.shift + 1 > 0 ? (q0 + a.shift + 1) / BN : 0);
     nfree = min(nfree, ntiles);
+    int tlo = 0, tfree = 0;
+    if (a.window > 0) {
+        const int qmax = min(q0 + BM, a.seq_q) - 1;
+        tlo = min(max(0, q0 - a.window + 1) / BN, ntiles);
+        tfree = max(tlo, (max(0, qmax - a.window + 1) + BN - 1) / BN);
+    }
 
     // byte offsets of this lane's tile copies (source side, swizzled) ...
     int kg[T::NI], vg[T::NI];
@@ -543,7 +560,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     st.m = -INFINITY;
     st.l = 0.0f;
 
-    if (ntiles > 0) prefill_copy_tile<D>(a, kbase, vbase, 0, kg, vg, k0s, v0s, wave);
+    // tile t lives in buffer t % 2
+    if (tlo < ntiles)
+        prefill_copy_tile<D>(a, kbase, vbase, tlo * BN, kg, vg, (tlo & 1) ? k1s : k0s, (tlo & 1) ? v1s : v0s, wave);
     wait_tile_copies();
     __syncthreads();
     // One tile: copy the next tile into the other buffers, compute this one, then
@@ -558,7 +577,24 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         wait_tile_copies();
         __syncthreads();
     };
-    int it = 0;
+    auto tile_masked = [&](int it) __attribute__((always_inline)) {
+        const int kv0 = it * BN;
+        const bool odd = it & 1;
+        if (it + 1 < ntiles)
+            prefill_copy_tile<D>(a, kbase, vbase, kv0 + BN, kg, vg, odd ? k0s : k1s, odd ? v0s : v1s, wave);
+        // waves whose queries all precede this tile, or whose windows all start
+        // past it, skip it
+        if ((!a.causal || kv0 <= qlast + a.shift) && (a.window <= 0 || kv0 + BN - 1 >= qfirst - a.window + 1))
+            prefill_step<DT, D>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
+        wait_tile_copies();
+        __syncthreads();
+    };
+    int it = tlo;
+    for (; it < tfree && it < ntiles; ++it) tile_masked(it);   // the window's lower edge
+    if (it < nfree && (it & 1)) {   // the paired loop below starts on an even tile
+        tile_free(it, k1s, v1s, k0s, v0s);
+        ++it;
+    }
     for (; it + 1 < nfree; it += 2) {
         tile_free(it, k0s, v0s, k1s, v1s);
         tile_free(it + 1, k1s, v1s, k0s, v0s);
@@ -567,17 +603,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         tile_free(it, k0s, v0s, k1s, v1s);
         ++it;
     }
-    for (; it < ntiles; ++it) {
-        const int kv0 = it * BN;
-        const bool odd = it & 1;
-        if (it + 1 < ntiles)
-            prefill_copy_tile<D>(a, kbase, vbase, kv0 + BN, kg, vg, odd ? k0s : k1s, odd ? v0s : v1s, wave);
-        // waves whose queries all precede this tile skip it
-        if (!a.causal || kv0 <= qlast + a.shift)
-            prefill_step<DT, D>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
-        wait_tile_copies();
-        __syncthreads();
-    }
+    for (; it < ntiles; ++it) tile_masked(it);
 
     // normalise and store: lane holds O[qi][32d + 8*(r/4) + 4g + r%4]
     const float ltot = swap_halves_sum(st.l);
@@ -597,8 +623,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
-    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || (m.dim != 128 && m.dim != 64) || m.window > 0 ||
-        m.alibi != 0.0f)
+    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || (m.dim != 128 && m.dim != 64) || m.alibi != 0.0f)
         return false;
     if (m.dim == 64 && m.seq_q == 1) return false;   // one query row: the general kernel (no 127 padding rows)
     if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF)
@@ -622,6 +647,9 @@ bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status
     a.qtiles = (int)((m.seq_q + fa::BM - 1) / fa::BM);
     a.causal = m.causal;
     a.shift = (int)m.shift;
+    // a window of seq_q or more hides no key (a query's distance to a visible key
+    // is below seq_q): run it as no window
+    a.window = (m.window > 0 && m.window < m.seq_q) ? (int)m.window : 0;
     a.xcd_map = ((a.batch * a.kv_heads) % 8 == 0) ? 1 : 0;
     a.scale_log2 = m.scale * 1.4426950408889634f;
     const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;

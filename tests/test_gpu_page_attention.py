@@ -377,6 +377,61 @@ def test_prefill_mfma_shapes(backend, dt, d, b, sq, sk, h, kvh, causal):
             assert np.all(got[i][:sq - sk] == 0)
 
 
+@pytest.mark.parametrize("b,sq,sk,h,kvh,causal,window", [
+    (1, 1024, 1024, 8, 2, True, 128),   # sliding_window_attention's window: tile-aligned edge
+    (2, 333, 333, 4, 1, True, 37),      # ragged edge inside tiles, partial tiles
+    (1, 300, 300, 4, 4, True, 1),       # each query sees only itself
+    (1, 200, 520, 4, 2, True, 200),     # seqK > seqQ: the edge trails the shifted diagonal
+    (1, 96, 40, 4, 2, True, 20),        # seqQ > seqK: leading queries see no key -> zeros
+    (1, 300, 77, 8, 8, False, 50),      # non-causal: queries past key 76 + 50 see no key
+    (1, 700, 700, 4, 2, False, 300),    # non-causal, edge crosses several tiles per block
+])
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_mfma_window(backend, dt, d, b, sq, sk, h, kvh, causal, window):
+    """Sliding-window prefill on the MFMA kernel (query q sees key k only if
+    q - k < window, typed_compute.go:172) against the oracle; rows with no
+    visible key are exactly zero."""
+    import puter_amd
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(310 + sq, (b, sq, h * d), 0.0, std), dt)
+    k = encode(seeded(311 + sk, (b, sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(312 + sk, (b, sk, kvh * d)), dt)
+    out = empty_dev((b, sq, h * d), np.uint16)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, window, 0.0, kvh)
+    backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, sq, sk, dt)
+    got = decode(to_host(out, np.uint16), dt)
+    O.set_threads(8)
+    shift = sk - sq
+    for i in range(b):
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, window=window, dtype=dt), dt)
+        assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"window prefill batch {i}")
+        for r in range(sq):
+            hi = min(sk - 1, r + shift) if causal else sk - 1
+            if max(0, r - window + 1) > hi:
+                assert np.all(got[i][r] == 0), f"row {r} sees no key"
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_mfma_wide_window_is_no_window(backend, d):
+    """A window wider than every query-key distance (seqQ or more) hides no key:
+    the output equals the windowless call bit for bit."""
+    import puter_amd
+    dt, s, h, kvh = O.BF16, 777, 8, 2
+    std = 1.0 / np.sqrt(d)
+    q = to_dev(encode(seeded(320, (s, h * d), 0.0, std), dt))
+    k = to_dev(encode(seeded(321, (s, kvh * d), 0.0, std), dt))
+    v = to_dev(encode(seeded(322, (s, kvh * d)), dt))
+    outs = []
+    for causal in (True, False):
+        for window in (0, s, 1 << 20):
+            out = empty_dev((s, h * d), np.uint16)
+            backend.MultiHeadAttention(puter_amd.MultiHeadAttentionConfig(h, d, causal, window, 0.0, kvh),
+                                       q, k, v, out, s, s, dt)
+            outs.append(to_host(out, np.uint16))
+        assert np.array_equal(outs[-3], outs[-2]) and np.array_equal(outs[-3], outs[-1])
+
+
 @pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
 @pytest.mark.parametrize("sq,sk,d,vd,causal", [
     (37, 37, 64, 64, True),
