@@ -445,12 +445,13 @@ namespace puter {
 
 // MultiHeadAttention with one query row per sequence (the reference's decode step:
 // gathered K/V, seqQ 1, typed_compute.go:206-237), bf16 or f16, head_dim 128, no
-// window or ALiBi: the paged decode kernels over the contiguous K/V (sequence b's keys are
+// ALiBi: the paged decode kernels over the contiguous K/V (sequence b's keys are
 // page b of seq_k rows), partials in the library's scratch.  A causal mask with
-// one query row sees every key (bottom-right alignment), as does no mask.
+// one query row sees every key (bottom-right alignment), as does no mask, and so
+// does a sliding window: it compares key indices with the query's row index
+// (typed_compute.go:172), 0 here, so q - k >= window holds for no key.
 bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
-    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || m.dim != 128 || m.seq_q != 1 || m.window > 0 ||
-        m.alibi != 0.0f)
+    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || m.dim != 128 || m.seq_q != 1 || m.alibi != 0.0f)
         return false;
     const int64_t G = m.heads / m.kv_heads;
     if (G != 1 && G != 2 && G != 4 && G != 8) return false;

@@ -1,5 +1,5 @@
 // MFMA flash-attention prefill: bf16 or f16 Q/K/V (prefill_kernel<dtype, head
-// dim>), f32 accumulation, output in the input format, head_dim 128 or 64, GQA,
+// dim, window>), f32 accumulation, output in the input format, head_dim 128 or 64, GQA,
 // optional causal mask: key k is visible to query q when
 // k <= q + shift.  MultiHeadAttention passes shift = seqK - seqQ (bottom-right
 // aligned, device/cpu/attention/typed_compute.go:166-168);
@@ -190,7 +190,7 @@ __device__ __forceinline__ f32x16 pf_mfma(typename PfFormat<DT>::V8 a, typename 
     else return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int DT, int D>
+template <int DT, int D, bool WIN>
 __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *ks, const char *vs,
                                              const typename PfFormat<DT>::V8 (&qf)[PfDim<D>::KS], PrefillState<D> &st,
                                              int qi, int kv0, const int (&ka)[PfDim<D>::KS],
@@ -220,16 +220,16 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
     if (masked) {
         // key kv0 + 32c + 8(r/4) + 4g + r%4 is visible iff its offset past
         // kv0 + 4g lies in [lo, lim] (the query's first and last visible keys,
-        // relative; the first is the sliding window's lower edge)
+        // relative; the first is the sliding window's lower edge, WIN only)
         const int last = a.causal ? min(qi + a.shift, a.seq_k - 1) : a.seq_k - 1;
         const int lim = last - kv0 - 4 * g;
-        const int lo = (a.window > 0 ? qi - a.window + 1 : 0) - kv0 - 4 * g;
+        const int lo = WIN ? qi - a.window + 1 - kv0 - 4 * g : 0;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 32 * c + 8 * (r >> 2) + (r & 3);
-                s[c][r] = (off > lim || off < lo) ? -INFINITY : s[c][r];
+                s[c][r] = (off > lim || (WIN && off < lo)) ? -INFINITY : s[c][r];
             }
     }
     // Fast path: every lane already has a reference and p = exp2(s*c - m) is
@@ -451,7 +451,9 @@ __device__ __forceinline__ void prefill_step_pipelined(const PrefillArgs &a, con
     }
 }
 
-template <int DT, int D>
+// WIN: a sliding window is set (a.window > 0); without one the window code
+// compiles away
+template <int DT, int D, bool WIN>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     using namespace fa;
     using T = PfDim<D>;
@@ -521,7 +523,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     if (a.causal) nfree = min(nfree, q0 + a.shift + 1 > 0 ? (q0 + a.shift + 1) / BN : 0);
     nfree = min(nfree, ntiles);
     int tlo = 0, tfree = 0;
-    if (a.window > 0) {
+    if (WIN) {
         const int qmax = min(q0 + BM, a.seq_q) - 1;
         tlo = min(max(0, q0 - a.window + 1) / BN, ntiles);
         tfree = max(tlo, (max(0, qmax - a.window + 1) + BN - 1) / BN);
@@ -584,8 +586,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             prefill_copy_tile<D>(a, kbase, vbase, kv0 + BN, kg, vg, odd ? k0s : k1s, odd ? v0s : v1s, wave);
         // waves whose queries all precede this tile, or whose windows all start
         // past it, skip it
-        if ((!a.causal || kv0 <= qlast + a.shift) && (a.window <= 0 || kv0 + BN - 1 >= qfirst - a.window + 1))
-            prefill_step<DT, D>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
+        if ((!a.causal || kv0 <= qlast + a.shift) && (!WIN || kv0 + BN - 1 >= qfirst - a.window + 1))
+            prefill_step<DT, D, WIN>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
         wait_tile_copies();
         __syncthreads();
     };
@@ -654,12 +656,24 @@ bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status
     a.scale_log2 = m.scale * 1.4426950408889634f;
     const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;
     if (blocks > 0x7FFFFFFF) return false;
+    const bool bf = dtype == PUTER_BF16, win = a.window > 0;
+    const dim3 grid((unsigned)blocks);
     if (m.dim == 128) {
-        if (dtype == PUTER_BF16) prefill_kernel<PUTER_BF16, 128><<<(unsigned)blocks, 256, 0, s>>>(a);
-        else prefill_kernel<PUTER_F16, 128><<<(unsigned)blocks, 256, 0, s>>>(a);
+        if (win) {
+            if (bf) prefill_kernel<PUTER_BF16, 128, true><<<grid, 256, 0, s>>>(a);
+            else prefill_kernel<PUTER_F16, 128, true><<<grid, 256, 0, s>>>(a);
+        } else {
+            if (bf) prefill_kernel<PUTER_BF16, 128, false><<<grid, 256, 0, s>>>(a);
+            else prefill_kernel<PUTER_F16, 128, false><<<grid, 256, 0, s>>>(a);
+        }
     } else {
-        if (dtype == PUTER_BF16) prefill_kernel<PUTER_BF16, 64><<<(unsigned)blocks, 256, 0, s>>>(a);
-        else prefill_kernel<PUTER_F16, 64><<<(unsigned)blocks, 256, 0, s>>>(a);
+        if (win) {
+            if (bf) prefill_kernel<PUTER_BF16, 64, true><<<grid, 256, 0, s>>>(a);
+            else prefill_kernel<PUTER_F16, 64, true><<<grid, 256, 0, s>>>(a);
+        } else {
+            if (bf) prefill_kernel<PUTER_BF16, 64, false><<<grid, 256, 0, s>>>(a);
+            else prefill_kernel<PUTER_F16, 64, false><<<grid, 256, 0, s>>>(a);
+        }
     }
     *status = check_launch("prefill mfma");
     return true;

@@ -249,16 +249,19 @@ def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
 
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
-@pytest.mark.parametrize("b,sk,h,kvh,causal", [
-    (1, 4096, 32, 8, True),     # configs[4]'s heads at one sequence's full context
-    (1, 100, 8, 8, False),      # group size 1, part of one split
-    (1, 300, 16, 2, True),      # group size 8
-    (3, 700, 8, 4, True),       # batched, partial last split
-    (64, 2000, 32, 8, True),    # 256-token splits (enough waves)
+@pytest.mark.parametrize("b,sk,h,kvh,causal,window", [
+    (1, 4096, 32, 8, True, 0),     # configs[4]'s heads at one sequence's full context
+    (1, 100, 8, 8, False, 0),      # group size 1, part of one split
+    (1, 300, 16, 2, True, 0),      # group size 8
+    (3, 700, 8, 4, True, 0),       # batched, partial last split
+    (64, 2000, 32, 8, True, 0),    # 256-token splits (enough waves)
+    (2, 900, 16, 4, True, 128),    # sliding_window_attention's window: hides no key of row 0
 ])
-def test_mha_one_query_row(backend, dt, b, sk, h, kvh, causal):
+def test_mha_one_query_row(backend, dt, b, sk, h, kvh, causal, window):
     """seqQ = 1 (the reference's decode step after KVPageGather) runs on the paged
-    decode kernels over contiguous K/V: against the oracle's MHA per sequence."""
+    decode kernels over contiguous K/V: against the oracle's MHA per sequence.  The
+    window compares keys with the query's row index (typed_compute.go:172), 0
+    for one row, so it masks nothing."""
     import puter_amd
     d = 128
     std = 1.0 / np.sqrt(d)
@@ -266,14 +269,14 @@ def test_mha_one_query_row(backend, dt, b, sk, h, kvh, causal):
     k = encode(seeded(701 + sk, (b, sk, kvh * d), 0.0, std), dt)
     v = encode(seeded(702 + sk, (b, sk, kvh * d)), dt)
     out = empty_dev((b, 1, h * d), np.uint16)
-    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, 0, 0.0, kvh)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, window, 0.0, kvh)
     if b == 1:
         backend.MultiHeadAttention(cfg, to_dev(q[0]), to_dev(k[0]), to_dev(v[0]), out, 1, sk, dt)
     else:
         backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, 1, sk, dt)
     got = decode(to_host(out, np.uint16), dt)
     for i in range(b):
-        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, dtype=dt), dt)
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, window=window, dtype=dt), dt)
         assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"one-row mha sequence {i}")
 
 
