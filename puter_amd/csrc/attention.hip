@@ -6,7 +6,8 @@
 // out[d] = sum_k p_k v[k, d]; an all-masked row yields zeros (softmax.go:33-75).
 //
 // This file holds the general kernel (one block per (batch, head, query row),
-// online softmax over 256-key chunks staged in LDS, f32 accumulation) and the
+// online softmax over 256-key chunks, one key's score per thread, P.V split over
+// all 256 threads for head dims up to 128, f32 accumulation) and the
 // dispatch: one query row in bf16 / f16 at head dim 128 goes to the split-K
 // decode kernels (decode.hip); bf16 / f16 causal or non-causal prefill at head
 // dim 128 or 64, with or without a sliding window, no ALiBi, to the MFMA flash
@@ -21,6 +22,7 @@ __global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {
     __shared__ float qrow[256];
     __shared__ float pk[256];
     __shared__ float red[4];
+    __shared__ float accs[256];
     const int64_t qi = blockIdx.x;
     const int64_t h = blockIdx.y;
     const int64_t b = blockIdx.z;
@@ -35,6 +37,11 @@ __global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {
     T *O = reinterpret_cast<T *>(a.o) + (b * a.seq_q + qi) * qs + h * D;
     for (int64_t d = tid; d < D; d += 256) qrow[d] = Elem<DT>::load(Q[d]);
     __syncthreads();
+    // P.V: thread tid sums output dim tid % DR over the keys j of each chunk with
+    // j % parts == tid / DR (parts = 256 / DR independent partial sums for D <= 128,
+    // added in part order at the end)
+    const int DR = D <= 64 ? 64 : D <= 128 ? 128 : 256;
+    const int parts = 256 / DR, dd = tid % DR, part = tid / DR;
     // keys visible to this row form [k_lo, k_hi)
     int64_t k_hi = a.seq_k;
     if (a.causal) k_hi = min(k_hi, qi + a.shift + 1);
@@ -67,16 +74,32 @@ __global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {
         ps = red[0] + red[1] + red[2] + red[3];
         const float alpha = (m == -INFINITY) ? 0.0f : expf(m - m_new);
         l = l * alpha + ps;
-        if (tid < D) {
-            float part = 0.0f;
+        if (dd < D) {
+            float pp = 0.0f;
             const int64_t n = min((int64_t)256, k_hi - c0);
-            for (int64_t j = 0; j < n; ++j) part += pk[j] * Elem<DT>::load(V[(c0 + j) * ks + tid]);
-            acc = acc * alpha + part;
+            // four loads in flight per step (a loop with a run-time stride is not
+            // unrolled by the compiler), products added in key order
+            int64_t j = part;
+            for (; j + 3 * parts < n; j += 4 * parts) {
+                float vv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) vv[u] = Elem<DT>::load(V[(c0 + j + u * parts) * ks + dd]);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) pp += pk[j + u * parts] * vv[u];
+            }
+            for (; j < n; j += parts) pp += pk[j] * Elem<DT>::load(V[(c0 + j) * ks + dd]);
+            acc = acc * alpha + pp;
         }
         m = m_new;
         __syncthreads();
     }
-    if (tid < D) O[tid] = Elem<DT>::store(l > 0.0f ? acc / l : 0.0f);
+    accs[tid] = acc;
+    __syncthreads();
+    if (tid < D) {
+        float t = accs[tid];
+        for (int p = 1; p < parts; ++p) t += accs[p * DR + tid];
+        O[tid] = Elem<DT>::store(l > 0.0f ? t / l : 0.0f);
+    }
 }
 
 static int run_mha(const puter_mha_config *config, const void *q, const void *k, const void *v,

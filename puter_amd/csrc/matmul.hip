@@ -36,8 +36,10 @@
 // kernel (one thread per output, f32 accumulation in index order).
 //
 // f32: 64 x 64 output tile per 256-thread block, 16-deep K slices in LDS, 4 x 4
-// register micro-tile, f32 FMA; grids of fewer than 256 tiles split K across
-// blocks (f32 partials summed in chunk order).  f64: one thread per output, f64 sum in index
+// register micro-tile, f32 FMA; grids of fewer than 256 tiles take the small
+// kernel (32 x 32 tiles, K split over the 8 waves of each block on the f32 MFMA)
+// when K is short for the tile count, else split K across blocks (f32 partials
+// summed in chunk order).  f64: one thread per output, f64 sum in index
 // order (matmulFloat64Scalar, device/cpu/matmul/select_generic.go:39-...).
 #include "common.hpp"
 #include <algorithm>
@@ -97,6 +99,66 @@ __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out
                 else out[r * N + c] = acc[i][j];
             }
         }
+}
+
+// f32, small outputs: one 512-thread block (8 waves) per 32 x 32 output tile, the
+// 8 waves splitting K into 8 runs of kw (a multiple of 64) and summing theirs on
+// v_mfma_f32_32x32x2_f32 (lane l: row / column l % 32; in step i of a 64-deep
+// chunk k0, half h = l / 32 takes k = k0 + 32h + i, so a lane's A values are 32
+// consecutive floats of its row and the B row k is read by 32 lanes at once);
+// the 8 partial tiles meet in LDS and are added in wave order.  One launch, no
+// partials in global memory: the cross-block split below spends as long on
+// writing and summing partials as on the products at these sizes.
+// VEC: A is 16-byte aligned and K % 4 == 0 (A rows read as float4).
+typedef float sm_f32x16 __attribute__((ext_vector_type(16)));
+constexpr int kSmallWaves = 8;
+
+template <bool VEC>
+__global__ __launch_bounds__(512) void matmul_f32_small_kernel(float *__restrict__ out, const float *__restrict__ A,
+                                                               const float *__restrict__ B, int64_t M, int64_t K,
+                                                               int64_t N, int64_t kw) {
+    __shared__ float part[kSmallWaves][32][33];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 31, h = lane >> 5;
+    const int64_t row = (int64_t)blockIdx.y * 32 + r, col = (int64_t)blockIdx.x * 32 + r;
+    const bool rok = row < M, cok = col < N;
+    const int64_t kb = (int64_t)wave * kw, ke = std::min(K, kb + kw);
+    const float *arow = A + (rok ? row : 0) * K;
+    sm_f32x16 acc = {};
+    for (int64_t k0 = kb; k0 < ke; k0 += 64) {
+        const int64_t kh = k0 + 32 * h;  // this lane's 32 k's: kh .. kh + 31
+        float a[32], b[32];
+        if constexpr (VEC) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int64_t k = kh + 4 * q;  // K % 4 == 0: a group is all in or all out
+                const float4 v = (rok && k < ke) ? *reinterpret_cast<const float4 *>(arow + k) : make_float4(0, 0, 0, 0);
+                a[4 * q] = v.x;
+                a[4 * q + 1] = v.y;
+                a[4 * q + 2] = v.z;
+                a[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) a[i] = (rok && kh + i < ke) ? arow[kh + i] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) b[i] = (cok && kh + i < ke) ? B[(kh + i) * N + col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc, 0, 0, 0);
+    }
+    // accumulator register j of lane l holds row 8(j/4) + 4h + j%4, column l % 32
+#pragma unroll
+    for (int j = 0; j < 16; ++j) part[wave][8 * (j >> 2) + 4 * h + (j & 3)][r] = acc[j];
+    __syncthreads();
+    for (int o = threadIdx.x; o < 32 * 32; o += 512) {
+        const int i = o >> 5, c = o & 31;
+        const int64_t gr = (int64_t)blockIdx.y * 32 + i, gc = (int64_t)blockIdx.x * 32 + c;
+        float t = part[0][i][c];
+#pragma unroll
+        for (int w = 1; w < kSmallWaves; ++w) t += part[w][i][c];
+        if (gr < M && gc < N) out[gr * N + gc] = t;
+    }
 }
 
 // ------------------------------------------------------- generic / f64 --
@@ -709,7 +771,7 @@ __global__ __launch_bounds__(256) void matmul_splitk_reduce_f32_kernel(float *c,
     }
 }
 
-// f32: 64 x 64 tiles; grids of fewer than 256 tiles split K (16-deep steps) into as
+// f32: 64 x 64 tiles; grids of fewer than 256 tiles take the small kernel or split K (16-deep steps) into as
 // many chunks as keep the grid within 512 blocks, each chunk at least two steps
 // deep (one-step chunks spent more time writing and summing partials than
 // computing: 128x512x512 18.3 -> 12.9 us), partials in the split-K scratch.
@@ -718,6 +780,20 @@ static int launch_matmul_f32(float *out, const float *left, const float *right, 
     const dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
     if (grid.y > 65535) return fail(PUTER_ERR_INVALID, "matmul: too many rows");
     const int64_t tiles = (int64_t)grid.x * grid.y, steps = (K + kDepth - 1) / kDepth;
+    const int64_t tiles32 = ((N + 31) / 32) * ((M + 31) / 32);
+    // small output, moderate depth: one launch splitting K inside each block, used
+    // while each wave's 64-deep steps (run one after another) number at most
+    // max(2, tiles32 / 32): a longer K over few tiles is faster split across blocks
+    // (32x8192x1024: 92 against 54 us)
+    const int64_t kw = ((K + kSmallWaves - 1) / kSmallWaves + 63) / 64 * 64;
+    if (tiles < 256 && tiles32 >= 32 && K >= 128 && kw / 64 <= std::max<int64_t>(2, tiles32 / 32)) {
+        const dim3 g32((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+        if (aligned16(left) && K % 4 == 0)
+            matmul_f32_small_kernel<true><<<g32, 512, 0, s>>>(out, left, right, M, K, N, kw);
+        else
+            matmul_f32_small_kernel<false><<<g32, 512, 0, s>>>(out, left, right, M, K, N, kw);
+        return check_launch("matmul");
+    }
     int64_t chunks = tiles < 256 ? std::max<int64_t>(std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(512 / tiles, 1), steps / 2), 64), 1) : 1;
     const int64_t per = (steps + chunks - 1) / chunks;
     chunks = (steps + per - 1) / per;

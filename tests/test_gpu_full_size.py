@@ -1,4 +1,4 @@
-"""GPU tier at BASELINE's full sizes.  The oracle cannot recompute these whole
+"""GPU tier at the full sizes of BASELINE.json's configs.  The oracle cannot recompute these whole
 in a test's time, so each case checks sampled rows / sequences against the
 oracle (every sampled row spans the tensor's full width, and the samples sit at
 the ends and in the middle, where indexing past 2^31 bytes or a wrong block

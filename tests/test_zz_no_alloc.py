@@ -33,7 +33,8 @@ def _operands(dt, m, k, n, seed):
     # 16 MiB of partials), then a smaller split-K shape and a ragged one
     (O.BF16, [(64, 4096, 4096), (16, 1024, 512), (5, 256, 136)]),
     (O.F16, [(64, 2048, 1024), (33, 512, 264)]),
-    # f32 split-K path (grids under 256 tiles), then smaller
+    # f32: K split inside each block (128x512x512, no scratch), then K split
+    # across blocks with partials in the scratch (32x256x128), then a tiny one
     (O.F32, [(128, 512, 512), (32, 256, 128), (7, 13, 5)]),
 ])
 def test_noalloc_matmul_matches_matmul(backend, dt, shapes):
