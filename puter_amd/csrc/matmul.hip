@@ -424,6 +424,63 @@ static int launch_mfma(void *out, const void *left, const void *right, int64_t M
     return 0;
 }
 
+// ------------------------------------------------ small outputs, 16-bit --
+// The 16-bit counterpart of matmul_f32_small_kernel: one 512-thread block per
+// 32 x 32 output tile, its 8 waves splitting K into runs of kw (a multiple of
+// 64) on v_mfma_f32_32x32x16 (in a 64-deep chunk k0, half h = lane / 32 takes
+// k0 + 32h .. +31: MFMA q gets k0 + 32h + 8q .. +7, so a lane's A values are
+// four 16-byte runs of its row and each B row is read by 32 lanes at once);
+// the 8 partial tiles meet in LDS, are added in wave order and rounded once.
+// Requires K % 8 == 0 and A 16-byte aligned.
+template <int DT>
+__global__ __launch_bounds__(512) void matmul16_small_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ A,
+                                                             const uint16_t *__restrict__ B, int64_t M, int64_t K,
+                                                             int64_t N, int64_t kw) {
+    __shared__ float part[kSmallWaves][32][33];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 31, h = lane >> 5;
+    const int64_t row = (int64_t)blockIdx.y * 32 + r, col = (int64_t)blockIdx.x * 32 + r;
+    const bool rok = row < M, cok = col < N;
+    const int64_t kb = (int64_t)wave * kw, ke = std::min(K, kb + kw);
+    const uint16_t *arow = A + (rok ? row : 0) * K;
+    mm_f32x16 acc = {};
+    for (int64_t k0 = kb; k0 < ke; k0 += 64) {
+        const int64_t kh = k0 + 32 * h;
+        uint4 a[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // K % 8 == 0: an 8-run is all in or all out
+            const int64_t k = kh + 8 * q;
+            a[q] = (rok && k < ke) ? *reinterpret_cast<const uint4 *>(arow + k) : make_uint4(0, 0, 0, 0);
+        }
+        uint32_t bv[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) bv[i] = (cok && kh + i < ke) ? B[(kh + i) * N + col] : 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 b = make_uint4(bv[8 * q] | (bv[8 * q + 1] << 16), bv[8 * q + 2] | (bv[8 * q + 3] << 16),
+                                       bv[8 * q + 4] | (bv[8 * q + 5] << 16), bv[8 * q + 6] | (bv[8 * q + 7] << 16));
+            if constexpr (DT == PUTER_BF16)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mm_bf16x8, a[q]),
+                                                              __builtin_bit_cast(mm_bf16x8, b), acc, 0, 0, 0);
+            else
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mm_f16x8, a[q]),
+                                                             __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
+        }
+    }
+    // accumulator register j of lane l holds row 8(j/4) + 4h + j%4, column l % 32
+#pragma unroll
+    for (int j = 0; j < 16; ++j) part[wave][8 * (j >> 2) + 4 * h + (j & 3)][r] = acc[j];
+    __syncthreads();
+    for (int o = threadIdx.x; o < 32 * 32; o += 512) {
+        const int i = o >> 5, c = o & 31;
+        const int64_t gr = (int64_t)blockIdx.y * 32 + i, gc = (int64_t)blockIdx.x * 32 + c;
+        float t = part[0][i][c];
+#pragma unroll
+        for (int w = 1; w < kSmallWaves; ++w) t += part[w][i][c];
+        if (gr < M && gc < N) out[gr * N + gc] = Elem<DT>::store(t);
+    }
+}
+
 // ---------------------------------------------------------- skinny (M <= 512) --
 // Decode-time projections (a few rows against a large weight matrix) are bound by
 // streaming `right` once.  A 256-thread block computes a 64 x 128 tile over one
@@ -741,6 +798,22 @@ template <int DT>
 static int launch_matmul16(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
                            hipStream_t s, PartialsTarget tgt) {
     if (N % 8 == 0 && K % 8 == 0 && aligned16(out) && aligned16(left) && aligned16(right)) {
+        // small outputs of moderate depth with a small right operand: K split inside
+        // each block (as for f32; 128x512x512 7.5 -> 6.3 us, 256x1024x1024 17.5 ->
+        // 10.0).  Its B reads are 2-byte gathers, so a few rows against a large
+        // weight stay on the skinny kernel (64x4096x4096: 52.7 against 17.5 us), as
+        // do shapes under 128 rows (level or slower) and over 256 (512x1024x1024:
+        // 18.4 against 16.2)
+        const int64_t tiles32 = ((N + 31) / 32) * ((M + 31) / 32);
+        const int64_t kw = ((K + kSmallWaves - 1) / kSmallWaves + 63) / 64 * 64;
+        const int64_t sk_tiles = ((M + sk::BM - 1) / sk::BM) * ((N + sk::BN - 1) / sk::BN);
+        if (M >= 128 && M <= 256 && K * N <= ((int64_t)1 << 22) && sk_tiles < 256 && tiles32 >= 32 && K >= 128 &&
+            kw / 64 <= std::max<int64_t>(2, tiles32 / 32)) {
+            const dim3 g32((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+            matmul16_small_kernel<DT><<<g32, 512, 0, s>>>(static_cast<uint16_t *>(out), static_cast<const uint16_t *>(left),
+                                                          static_cast<const uint16_t *>(right), M, K, N, kw);
+            return check_launch("matmul");
+        }
         if (M <= 512) {
             const int rc = launch_skinny<DT>(out, left, right, M, K, N, s, tgt);
             if (rc != 1) return rc;

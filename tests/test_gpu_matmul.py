@@ -55,7 +55,9 @@ def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
 def test_matmul_16bit_skinny_split_k(backend, dt, rows, inner, cols):
     """rows <= 512 take the split-K kernel (64 x 128 tiles over chunks of K, f32
     partials summed in chunk order): ragged rows / columns, K tails, one-chunk and
-    many-chunk splits.  Oracle rows sampled across the tile bands (all columns),
+    many-chunk splits; 200 x 1000 x 1024 (128 to 256 rows, a right operand of at
+    most 2^22 elements) takes the small kernel instead, K split over the 8 waves of
+    each block, as do 256x256x128 and 128x512x512 above.  Oracle rows sampled across the tile bands (all columns),
     numpy's f64 product for the whole output, and two calls bit-identical."""
     a = O.from_f32(seeded(rows * 3 + inner, (rows, inner)), dt)
     b = O.from_f32(seeded(cols * 7 + inner, (inner, cols), 0.0, 0.05), dt)
