@@ -45,6 +45,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 namespace puter {
 
@@ -101,36 +102,44 @@ __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out
         }
 }
 
-// f32, small outputs: one 512-thread block (8 waves) per 32 x 32 output tile, the
-// 8 waves splitting K into 8 runs of kw (a multiple of 64) and summing theirs on
-// v_mfma_f32_32x32x2_f32 (lane l: row / column l % 32; in step i of a 64-deep
-// chunk k0, half h = l / 32 takes k = k0 + 32h + i, so a lane's A values are 32
-// consecutive floats of its row and the B row k is read by 32 lanes at once);
-// the 8 partial tiles meet in LDS and are added in wave order.  One launch, no
+// f32, small outputs: one 512-thread block (8 waves) per TM x TM output tile
+// (TM = 32 or 16), the 8 waves splitting K into 8 runs of kw (a multiple of 64)
+// and summing theirs on the f32 MFMA: TM = 32 on v_mfma_f32_32x32x2_f32 (lane l:
+// row / column l % 32; in step i of a 64-deep chunk k0, half h = l / 32 takes
+// k = k0 + 32h + i), TM = 16 on v_mfma_f32_16x16x4_f32 (row / column l % 16;
+// quarter q = l / 16 takes k = k0 + 16q + i).  A lane's A values are thus
+// consecutive floats of its row and each B row is read by TM lanes at once.  The
+// 8 partial tiles meet in LDS and are added in wave order.  One launch, no
 // partials in global memory: the cross-block split below spends as long on
-// writing and summing partials as on the products at these sizes.
+// writing and summing partials as on the products at these sizes.  16 x 16 tiles
+// spread a small output over four times the CUs (128x512x512: 7.4 -> 4.1 us with
+// them) but re-read the operands more (256x1024x1024: 13.2 against 16.0 us), so
+// they serve outputs of fewer than 256 32 x 32 tiles.
 // VEC: A is 16-byte aligned and K % 4 == 0 (A rows read as float4).
 typedef float sm_f32x16 __attribute__((ext_vector_type(16)));
+typedef float sm_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSmallWaves = 8;
 
-template <bool VEC>
+template <int TM, bool VEC>
 __global__ __launch_bounds__(512) void matmul_f32_small_kernel(float *__restrict__ out, const float *__restrict__ A,
                                                                const float *__restrict__ B, int64_t M, int64_t K,
                                                                int64_t N, int64_t kw) {
-    __shared__ float part[kSmallWaves][32][33];
+    constexpr int KL = 64 / (64 / TM);   // k's per lane per 64-deep chunk: 32 (TM 32), 16 (TM 16)
+    using Acc = typename std::conditional<TM == 32, sm_f32x16, sm_f32x4>::type;
+    __shared__ float part[kSmallWaves][TM][TM + 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 31, h = lane >> 5;
-    const int64_t row = (int64_t)blockIdx.y * 32 + r, col = (int64_t)blockIdx.x * 32 + r;
+    const int r = lane % TM, h = lane / TM;
+    const int64_t row = (int64_t)blockIdx.y * TM + r, col = (int64_t)blockIdx.x * TM + r;
     const bool rok = row < M, cok = col < N;
     const int64_t kb = (int64_t)wave * kw, ke = std::min(K, kb + kw);
     const float *arow = A + (rok ? row : 0) * K;
-    sm_f32x16 acc = {};
+    Acc acc = {};
     for (int64_t k0 = kb; k0 < ke; k0 += 64) {
-        const int64_t kh = k0 + 32 * h;  // this lane's 32 k's: kh .. kh + 31
-        float a[32], b[32];
+        const int64_t kh = k0 + KL * h;  // this lane's k's: kh .. kh + KL - 1
+        float a[KL], b[KL];
         if constexpr (VEC) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
+            for (int q = 0; q < KL / 4; ++q) {
                 const int64_t k = kh + 4 * q;  // K % 4 == 0: a group is all in or all out
                 const float4 v = (rok && k < ke) ? *reinterpret_cast<const float4 *>(arow + k) : make_float4(0, 0, 0, 0);
                 a[4 * q] = v.x;
@@ -140,20 +149,25 @@ __global__ __launch_bounds__(512) void matmul_f32_small_kernel(float *__restrict
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 32; ++i) a[i] = (rok && kh + i < ke) ? arow[kh + i] : 0.0f;
+            for (int i = 0; i < KL; ++i) a[i] = (rok && kh + i < ke) ? arow[kh + i] : 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < 32; ++i) b[i] = (cok && kh + i < ke) ? B[(kh + i) * N + col] : 0.0f;
+        for (int i = 0; i < KL; ++i) b[i] = (cok && kh + i < ke) ? B[(kh + i) * N + col] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc, 0, 0, 0);
+        for (int i = 0; i < KL; ++i) {
+            if constexpr (TM == 32) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc, 0, 0, 0);
+            else acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[i], acc, 0, 0, 0);
+        }
     }
-    // accumulator register j of lane l holds row 8(j/4) + 4h + j%4, column l % 32
+    // accumulator register j of lane l holds column l % TM and row 8(j/4) + 4h + j%4
+    // (TM 32) or 4h + j (TM 16)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) part[wave][8 * (j >> 2) + 4 * h + (j & 3)][r] = acc[j];
+    for (int j = 0; j < (TM == 32 ? 16 : 4); ++j)
+        part[wave][TM == 32 ? 8 * (j >> 2) + 4 * h + (j & 3) : 4 * h + j][r] = acc[j];
     __syncthreads();
-    for (int o = threadIdx.x; o < 32 * 32; o += 512) {
-        const int i = o >> 5, c = o & 31;
-        const int64_t gr = (int64_t)blockIdx.y * 32 + i, gc = (int64_t)blockIdx.x * 32 + c;
+    for (int o = threadIdx.x; o < TM * TM; o += 512) {
+        const int i = o / TM, c = o % TM;
+        const int64_t gr = (int64_t)blockIdx.y * TM + i, gc = (int64_t)blockIdx.x * TM + c;
         float t = part[0][i][c];
 #pragma unroll
         for (int w = 1; w < kSmallWaves; ++w) t += part[w][i][c];
@@ -426,54 +440,68 @@ static int launch_mfma(void *out, const void *left, const void *right, int64_t M
 
 // ------------------------------------------------ small outputs, 16-bit --
 // The 16-bit counterpart of matmul_f32_small_kernel: one 512-thread block per
-// 32 x 32 output tile, its 8 waves splitting K into runs of kw (a multiple of
-// 64) on v_mfma_f32_32x32x16 (in a 64-deep chunk k0, half h = lane / 32 takes
-// k0 + 32h .. +31: MFMA q gets k0 + 32h + 8q .. +7, so a lane's A values are
-// four 16-byte runs of its row and each B row is read by 32 lanes at once);
-// the 8 partial tiles meet in LDS, are added in wave order and rounded once.
-// Requires K % 8 == 0 and A 16-byte aligned.
-template <int DT>
+// TM x TM output tile, its 8 waves splitting K into runs of kw (a multiple of
+// 64) on v_mfma_f32_32x32x16 (TM 32: in a 64-deep chunk k0, half h = lane / 32
+// takes k0 + 32h .. +31, MFMA q of the chunk k0 + 32h + 8q .. +7) or
+// v_mfma_f32_16x16x32 (TM 16: quarter h = lane / 16 takes k0 + 16h .. +15, MFMA q
+// k0 + 16h + 8q .. +7), so a lane's A values are 16-byte runs of its row and each
+// B row is read by TM lanes at once; the 8 partial tiles meet in LDS, are added
+// in wave order and rounded once.  Requires K % 8 == 0 and A 16-byte aligned.
+template <int DT, int TM>
 __global__ __launch_bounds__(512) void matmul16_small_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ A,
                                                              const uint16_t *__restrict__ B, int64_t M, int64_t K,
                                                              int64_t N, int64_t kw) {
-    __shared__ float part[kSmallWaves][32][33];
+    constexpr int KL = 64 / (64 / TM), NQ = KL / 8;   // k's per lane per chunk, MFMAs per chunk
+    using Acc = typename std::conditional<TM == 32, mm_f32x16, sm_f32x4>::type;
+    __shared__ float part[kSmallWaves][TM][TM + 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 31, h = lane >> 5;
-    const int64_t row = (int64_t)blockIdx.y * 32 + r, col = (int64_t)blockIdx.x * 32 + r;
+    const int r = lane % TM, h = lane / TM;
+    const int64_t row = (int64_t)blockIdx.y * TM + r, col = (int64_t)blockIdx.x * TM + r;
     const bool rok = row < M, cok = col < N;
     const int64_t kb = (int64_t)wave * kw, ke = std::min(K, kb + kw);
     const uint16_t *arow = A + (rok ? row : 0) * K;
-    mm_f32x16 acc = {};
+    Acc acc = {};
     for (int64_t k0 = kb; k0 < ke; k0 += 64) {
-        const int64_t kh = k0 + 32 * h;
-        uint4 a[4];
+        const int64_t kh = k0 + KL * h;
+        uint4 a[NQ];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {  // K % 8 == 0: an 8-run is all in or all out
+        for (int q = 0; q < NQ; ++q) {  // K % 8 == 0: an 8-run is all in or all out
             const int64_t k = kh + 8 * q;
             a[q] = (rok && k < ke) ? *reinterpret_cast<const uint4 *>(arow + k) : make_uint4(0, 0, 0, 0);
         }
-        uint32_t bv[32];
+        uint32_t bv[KL];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) bv[i] = (cok && kh + i < ke) ? B[(kh + i) * N + col] : 0u;
+        for (int i = 0; i < KL; ++i) bv[i] = (cok && kh + i < ke) ? B[(kh + i) * N + col] : 0u;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < NQ; ++q) {
             const uint4 b = make_uint4(bv[8 * q] | (bv[8 * q + 1] << 16), bv[8 * q + 2] | (bv[8 * q + 3] << 16),
                                        bv[8 * q + 4] | (bv[8 * q + 5] << 16), bv[8 * q + 6] | (bv[8 * q + 7] << 16));
-            if constexpr (DT == PUTER_BF16)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mm_bf16x8, a[q]),
-                                                              __builtin_bit_cast(mm_bf16x8, b), acc, 0, 0, 0);
-            else
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mm_f16x8, a[q]),
-                                                             __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
+            if constexpr (TM == 32) {
+                if constexpr (DT == PUTER_BF16)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mm_bf16x8, a[q]),
+                                                                  __builtin_bit_cast(mm_bf16x8, b), acc, 0, 0, 0);
+                else
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mm_f16x8, a[q]),
+                                                                 __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
+            } else {
+                if constexpr (DT == PUTER_BF16)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mm_bf16x8, a[q]),
+                                                                  __builtin_bit_cast(mm_bf16x8, b), acc, 0, 0, 0);
+                else
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mm_f16x8, a[q]),
+                                                                 __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
+            }
         }
     }
-    // accumulator register j of lane l holds row 8(j/4) + 4h + j%4, column l % 32
+    // accumulator register j of lane l holds column l % TM and row 8(j/4) + 4h + j%4
+    // (TM 32) or 4h + j (TM 16)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) part[wave][8 * (j >> 2) + 4 * h + (j & 3)][r] = acc[j];
+    for (int j = 0; j < (TM == 32 ? 16 : 4); ++j)
+        part[wave][TM == 32 ? 8 * (j >> 2) + 4 * h + (j & 3) : 4 * h + j][r] = acc[j];
     __syncthreads();
-    for (int o = threadIdx.x; o < 32 * 32; o += 512) {
-        const int i = o >> 5, c = o & 31;
-        const int64_t gr = (int64_t)blockIdx.y * 32 + i, gc = (int64_t)blockIdx.x * 32 + c;
+    for (int o = threadIdx.x; o < TM * TM; o += 512) {
+        const int i = o / TM, c = o % TM;
+        const int64_t gr = (int64_t)blockIdx.y * TM + i, gc = (int64_t)blockIdx.x * TM + c;
         float t = part[0][i][c];
 #pragma unroll
         for (int w = 1; w < kSmallWaves; ++w) t += part[w][i][c];
@@ -809,9 +837,15 @@ static int launch_matmul16(void *out, const void *left, const void *right, int64
         const int64_t sk_tiles = ((M + sk::BM - 1) / sk::BM) * ((N + sk::BN - 1) / sk::BN);
         if (M >= 128 && M <= 256 && K * N <= ((int64_t)1 << 22) && sk_tiles < 256 && tiles32 >= 32 && K >= 128 &&
             kw / 64 <= std::max<int64_t>(2, tiles32 / 32)) {
-            const dim3 g32((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
-            matmul16_small_kernel<DT><<<g32, 512, 0, s>>>(static_cast<uint16_t *>(out), static_cast<const uint16_t *>(left),
-                                                          static_cast<const uint16_t *>(right), M, K, N, kw);
+            uint16_t *o = static_cast<uint16_t *>(out);
+            const uint16_t *l = static_cast<const uint16_t *>(left), *r = static_cast<const uint16_t *>(right);
+            if (tiles32 < 256) {   // 16 x 16 tiles: four times the blocks
+                const dim3 g16((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
+                matmul16_small_kernel<DT, 16><<<g16, 512, 0, s>>>(o, l, r, M, K, N, kw);
+            } else {
+                const dim3 g32((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+                matmul16_small_kernel<DT, 32><<<g32, 512, 0, s>>>(o, l, r, M, K, N, kw);
+            }
             return check_launch("matmul");
         }
         if (M <= 512) {
@@ -860,11 +894,16 @@ static int launch_matmul_f32(float *out, const float *left, const float *right, 
     // (32x8192x1024: 92 against 54 us)
     const int64_t kw = ((K + kSmallWaves - 1) / kSmallWaves + 63) / 64 * 64;
     if (tiles < 256 && tiles32 >= 32 && K >= 128 && kw / 64 <= std::max<int64_t>(2, tiles32 / 32)) {
-        const dim3 g32((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
-        if (aligned16(left) && K % 4 == 0)
-            matmul_f32_small_kernel<true><<<g32, 512, 0, s>>>(out, left, right, M, K, N, kw);
-        else
-            matmul_f32_small_kernel<false><<<g32, 512, 0, s>>>(out, left, right, M, K, N, kw);
+        const bool vec = aligned16(left) && K % 4 == 0;
+        if (tiles32 < 256) {   // 16 x 16 tiles: four times the blocks
+            const dim3 g16((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
+            if (vec) matmul_f32_small_kernel<16, true><<<g16, 512, 0, s>>>(out, left, right, M, K, N, kw);
+            else matmul_f32_small_kernel<16, false><<<g16, 512, 0, s>>>(out, left, right, M, K, N, kw);
+        } else {
+            const dim3 g32((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32));
+            if (vec) matmul_f32_small_kernel<32, true><<<g32, 512, 0, s>>>(out, left, right, M, K, N, kw);
+            else matmul_f32_small_kernel<32, false><<<g32, 512, 0, s>>>(out, left, right, M, K, N, kw);
+        }
         return check_launch("matmul");
     }
     int64_t chunks = tiles < 256 ? std::max<int64_t>(std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(512 / tiles, 1), steps / 2), 64), 1) : 1;

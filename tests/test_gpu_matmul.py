@@ -212,6 +212,27 @@ def test_matmul_f32_split_k(backend, rows, inner, cols):
     assert np.array_equal(to_host(out2, np.float32), got)
 
 
+def test_matmul_f32_small_unaligned_left(backend):
+    """The small f32 kernel with A rows that are a whole number of 16-byte vectors
+    but an A base off by one float (the scalar-load variant): equal bit for bit to
+    the aligned call on the same values, and to the oracle at the f32 bar."""
+    import torch
+    rows, inner, cols = 128, 512, 512
+    a = seeded(77, (rows, inner))
+    b = seeded(78, (inner, cols), 0.0, 0.05)
+    ad, bd = to_dev(a), to_dev(b)
+    shifted = torch.empty(rows * inner + 1, dtype=torch.float32, device="cuda")
+    shifted[1:].copy_(ad.reshape(-1))
+    au = shifted[1:]                      # 4 bytes past a 16-byte boundary
+    assert au.data_ptr() % 16 == 4
+    out, out_u = empty_dev((rows, cols), np.float32), empty_dev((rows, cols), np.float32)
+    backend.Matmul(out, ad, bd, rows, inner, cols, O.F32)
+    backend.Matmul(out_u, au, bd, rows, inner, cols, O.F32)
+    got, got_u = to_host(out, np.float32), to_host(out_u, np.float32)
+    assert np.array_equal(got, got_u)
+    assert_close(got_u, O.matmul_f32(a, b), TOL[O.F32], elem_tol=1e-3, what="f32 matmul, unaligned A")
+
+
 @pytest.mark.parametrize("dt,np_dt", [(O.BF16, np.uint16), (O.F32, np.float32), (O.F64, np.float64)])
 def test_matmul_empty_inner_is_zero(backend, dt, np_dt):
     rows, cols = 5, 7   # odd element count
