@@ -55,7 +55,16 @@ __global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {
         if (k < k_hi) {
             const T *kr = K + k * ks;
             float dot = 0.0f;
-            for (int64_t d = 0; d < D; ++d) dot += qrow[d] * Elem<DT>::load(kr[d]);
+            // sixteen loads in flight per step, products added in index order
+            int64_t d = 0;
+            for (; d + 16 <= D; d += 16) {
+                float kv[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) kv[u] = Elem<DT>::load(kr[d + u]);
+#pragma unroll
+                for (int u = 0; u < 16; ++u) dot += qrow[d + u] * kv[u];
+            }
+            for (; d < D; ++d) dot += qrow[d] * Elem<DT>::load(kr[d]);
             s = round_reduction<DT>(dot) * a.scale;
             if (a.alibi != 0.0f) s += a.alibi * (float)(k - qi);
         }
@@ -77,15 +86,15 @@ __global__ __launch_bounds__(256) void mha_generic_kernel(MhaArgs a) {
         if (dd < D) {
             float pp = 0.0f;
             const int64_t n = min((int64_t)256, k_hi - c0);
-            // four loads in flight per step (a loop with a run-time stride is not
+            // eight loads in flight per step (a loop with a run-time stride is not
             // unrolled by the compiler), products added in key order
             int64_t j = part;
-            for (; j + 3 * parts < n; j += 4 * parts) {
-                float vv[4];
+            for (; j + 7 * parts < n; j += 8 * parts) {
+                float vv[8];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) vv[u] = Elem<DT>::load(V[(c0 + j + u * parts) * ks + dd]);
+                for (int u = 0; u < 8; ++u) vv[u] = Elem<DT>::load(V[(c0 + j + u * parts) * ks + dd]);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) pp += pk[j + u * parts] * vv[u];
+                for (int u = 0; u < 8; ++u) pp += pk[j + u * parts] * vv[u];
             }
             for (; j < n; j += parts) pp += pk[j] * Elem<DT>::load(V[(c0 + j) * ks + dd]);
             acc = acc * alpha + pp;
