@@ -787,9 +787,12 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
     if (tiles_n > 0x7FFFFFFF) return 1;
     const int64_t slices = (K + sk::BK - 1) / sk::BK;
     // as many chunks as keep the grid within one wave of 512 blocks (2 per CU): a
-    // partial second wave would run at a fraction of the bandwidth
+    // partial second wave would run at a fraction of the bandwidth; at most 8, as
+    // the partials written and summed grow with the chunk count (against at most
+    // 64: 64x4096x4096 18.1 -> 14.7 us, 32x2048x2048 17.2 -> 8.2, 1x4096x4096
+    // 11.0 -> 10.1; 4 lost on 64x14336x4096, 41.4 against 29.0)
     int64_t chunks = std::min<int64_t>(std::max<int64_t>(512 / (tiles_m * tiles_n), 1), slices);
-    chunks = std::min<int64_t>(chunks, 64);
+    chunks = std::min<int64_t>(chunks, 8);
     const int64_t per = (slices + chunks - 1) / chunks;  // slices per chunk
     chunks = (slices + per - 1) / per;
     SkArgs p{static_cast<const uint16_t *>(left), static_cast<const uint16_t *>(right), static_cast<uint16_t *>(out),

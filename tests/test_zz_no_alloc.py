@@ -29,9 +29,9 @@ def _operands(dt, m, k, n, seed):
 
 
 @pytest.mark.parametrize("dt,shapes", [
-    # 16-bit skinny split-K path: 64 x 4096 x 4096 (16 chunks x 32 tiles: the full
+    # 16-bit skinny split-K path: 128 x 4096 x 4096 (8 chunks x 64 tiles: the full
     # 16 MiB of partials), then a smaller split-K shape and a ragged one
-    (O.BF16, [(64, 4096, 4096), (16, 1024, 512), (5, 256, 136)]),
+    (O.BF16, [(128, 4096, 4096), (16, 1024, 512), (5, 256, 136)]),
     (O.F16, [(64, 2048, 1024), (33, 512, 264)]),
     # f32: K split inside each block (128x512x512, no scratch), then K split
     # across blocks with partials in the scratch (32x256x128), then a tiny one
