@@ -10,7 +10,7 @@
 // all 256 threads for head dims up to 128, f32 accumulation) and the
 // dispatch: one query row in bf16 / f16 at head dim 128 goes to the split-K
 // decode kernels (decode.hip); bf16 / f16 causal or non-causal prefill at head
-// dim 128 or 64, with or without a sliding window, no ALiBi, to the MFMA flash
+// dim 128 or 64, with or without a sliding window or ALiBi, to the MFMA flash
 // kernel (prefill.hip).
 #include "attention.hpp"
 

@@ -18,7 +18,7 @@ struct MhaArgs {
 };
 
 // MFMA flash prefill (prefill.hip).  Returns true and sets *status when the
-// shape is one it serves (bf16 / f16, head_dim 128 or 64, causal or not, sliding window, no ALiBi;
+// shape is one it serves (bf16 / f16, head_dim 128 or 64, causal or not, sliding window, ALiBi;
 // head dim 64 only for more than one query row).
 bool launch_prefill_mfma(const MhaArgs &a, int dtype, hipStream_t s, int *status);
 // one query row per sequence (bf16 / f16, head_dim 128): the paged decode kernels

@@ -6,7 +6,9 @@
 // ScaledDotProductAttention passes 0 (typed_compute.go:60-62).  Optional
 // sliding window: key k is visible to query q only when q - k < window
 // (typed_compute.go:172); a block skips the key tiles below its first query's
-// window and masks those below its last query's.
+// window and masks those below its last query's.  Optional ALiBi: the score
+// gains slope * (k - q) (typed_compute.go:176-178); every tile then takes the
+// masked step.
 //
 // Work split: one 256-thread block (4 wave64s) per (128-query tile, head,
 // batch); wave w owns 32 queries; two blocks share a CU (2 waves per SIMD, so
@@ -130,6 +132,7 @@ struct PrefillArgs {
     int causal, xcd_map;
     int shift;         // causal: key k visible to query q iff k <= q + shift
     int window;        // > 0: key k visible to query q only if k > q - window
+    float alibi_s;     // ALiBi slope / scale: the dot gains alibi_s * (k - q) before scaling
     float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -190,7 +193,7 @@ __device__ __forceinline__ f32x16 pf_mfma(typename PfFormat<DT>::V8 a, typename 
     else return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int DT, int D, bool WIN>
+template <int DT, int D, bool GEN>
 __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *ks, const char *vs,
                                              const typename PfFormat<DT>::V8 (&qf)[PfDim<D>::KS], PrefillState<D> &st,
                                              int qi, int kv0, const int (&ka)[PfDim<D>::KS],
@@ -220,16 +223,28 @@ __device__ __forceinline__ void prefill_step(const PrefillArgs &a, const char *k
     if (masked) {
         // key kv0 + 32c + 8(r/4) + 4g + r%4 is visible iff its offset past
         // kv0 + 4g lies in [lo, lim] (the query's first and last visible keys,
-        // relative; the first is the sliding window's lower edge, WIN only)
+        // relative; the first is the sliding window's lower edge, GEN only).  GEN
+        // also adds the ALiBi bias slope * (k - q) (as alibi_s * (k - q) before the
+        // scale), after the f16 rounding of the dot, as the reference adds it to
+        // the scaled score (typed_compute.go:176-178)
         const int last = a.causal ? min(qi + a.shift, a.seq_k - 1) : a.seq_k - 1;
         const int lim = last - kv0 - 4 * g;
-        const int lo = WIN ? qi - a.window + 1 - kv0 - 4 * g : 0;
+        const bool win = GEN && a.window > 0;
+        const int lo = win ? qi - a.window + 1 - kv0 - 4 * g : 0;
+        if (GEN && a.alibi_s != 0.0f) {
+            const float base = (float)(kv0 + 4 * g - qi);
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    s[c][r] += a.alibi_s * (base + (float)(32 * c + 8 * (r >> 2) + (r & 3)));
+        }
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int off = 32 * c + 8 * (r >> 2) + (r & 3);
-                s[c][r] = (off > lim || (WIN && off < lo)) ? -INFINITY : s[c][r];
+                s[c][r] = (off > lim || (win && off < lo)) ? -INFINITY : s[c][r];
             }
     }
     // Fast path: every lane already has a reference and p = exp2(s*c - m) is
@@ -451,9 +466,10 @@ __device__ __forceinline__ void prefill_step_pipelined(const PrefillArgs &a, con
     }
 }
 
-// WIN: a sliding window is set (a.window > 0); without one the window code
-// compiles away
-template <int DT, int D, bool WIN>
+// GEN: a sliding window (a.window > 0) or an ALiBi slope is set; without either
+// that code compiles away.  With ALiBi every tile takes the masked step, which
+// adds the bias.
+template <int DT, int D, bool GEN>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     using namespace fa;
     using T = PfDim<D>;
@@ -522,8 +538,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     int nfree = a.seq_k / BN;
     if (a.causal) nfree = min(nfree, q0 + a.shift + 1 > 0 ? (q0 + a.shift + 1) / BN : 0);
     nfree = min(nfree, ntiles);
+    if (GEN && a.alibi_s != 0.0f) nfree = 0;   // the bias is added by the masked step only
     int tlo = 0, tfree = 0;
-    if (WIN) {
+    if (GEN && a.window > 0) {
         const int qmax = min(q0 + BM, a.seq_q) - 1;
         tlo = min(max(0, q0 - a.window + 1) / BN, ntiles);
         tfree = max(tlo, (max(0, qmax - a.window + 1) + BN - 1) / BN);
@@ -586,8 +603,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             prefill_copy_tile<D>(a, kbase, vbase, kv0 + BN, kg, vg, odd ? k0s : k1s, odd ? v0s : v1s, wave);
         // waves whose queries all precede this tile, or whose windows all start
         // past it, skip it
-        if ((!a.causal || kv0 <= qlast + a.shift) && (!WIN || kv0 + BN - 1 >= qfirst - a.window + 1))
-            prefill_step<DT, D, WIN>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
+        if ((!a.causal || kv0 <= qlast + a.shift) && (!GEN || a.window <= 0 || kv0 + BN - 1 >= qfirst - a.window + 1))
+            prefill_step<DT, D, GEN>(a, odd ? k1s : k0s, odd ? v1s : v0s, qf, st, qi, kv0, ka, va, g, true);
         wait_tile_copies();
         __syncthreads();
     };
@@ -625,8 +642,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
-    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || (m.dim != 128 && m.dim != 64) || m.alibi != 0.0f)
-        return false;
+    if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || (m.dim != 128 && m.dim != 64)) return false;
     if (m.dim == 64 && m.seq_q == 1) return false;   // one query row: the general kernel (no 127 padding rows)
     if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF)
         return false;
@@ -652,11 +668,12 @@ bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status
     // a window of seq_q or more hides no key (a query's distance to a visible key
     // is below seq_q): run it as no window
     a.window = (m.window > 0 && m.window < m.seq_q) ? (int)m.window : 0;
+    a.alibi_s = m.alibi != 0.0f ? m.alibi / m.scale : 0.0f;
     a.xcd_map = ((a.batch * a.kv_heads) % 8 == 0) ? 1 : 0;
     a.scale_log2 = m.scale * 1.4426950408889634f;
     const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;
     if (blocks > 0x7FFFFFFF) return false;
-    const bool bf = dtype == PUTER_BF16, win = a.window > 0;
+    const bool bf = dtype == PUTER_BF16, win = a.window > 0 || a.alibi_s != 0.0f;
     const dim3 grid((unsigned)blocks);
     if (m.dim == 128) {
         if (win) {

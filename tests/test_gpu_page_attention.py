@@ -415,6 +415,33 @@ def test_prefill_mfma_window(backend, dt, d, b, sq, sk, h, kvh, causal, window):
                 assert np.all(got[i][r] == 0), f"row {r} sees no key"
 
 
+@pytest.mark.parametrize("b,sq,sk,h,kvh,causal,window,alibi", [
+    (1, 512, 512, 8, 2, True, 0, 0.25),      # causal ALiBi, distant keys fade out
+    (2, 333, 333, 4, 1, False, 0, 0.0625),   # non-causal: later keys gain, ragged tiles
+    (1, 200, 520, 4, 2, True, 100, 0.5),     # seqK > seqQ with a window and ALiBi
+    (1, 96, 40, 4, 4, True, 0, -0.125),      # negative slope; leading queries see no key
+])
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_mfma_alibi(backend, dt, d, b, sq, sk, h, kvh, causal, window, alibi):
+    """ALiBi prefill on the MFMA kernel (score += slope * (k - q) on the scaled
+    score, typed_compute.go:176-178; with or without a window) against the oracle."""
+    import puter_amd
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(330 + sq, (b, sq, h * d), 0.0, std), dt)
+    k = encode(seeded(331 + sk, (b, sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(332 + sk, (b, sk, kvh * d)), dt)
+    out = empty_dev((b, sq, h * d), np.uint16)
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, window, alibi, kvh)
+    backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, sq, sk, dt)
+    got = decode(to_host(out, np.uint16), dt)
+    O.set_threads(8)
+    for i in range(b):
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, window=window, alibi=alibi,
+                           dtype=dt), dt)
+        assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"alibi prefill batch {i}")
+
+
 @pytest.mark.parametrize("d", [128, 64])
 def test_prefill_mfma_wide_window_is_no_window(backend, d):
     """A window wider than every query-key distance (seqQ or more) hides no key:
