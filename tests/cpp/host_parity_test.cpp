@@ -202,11 +202,13 @@ CASE(kv_page_write_gather_and_status) {
 }
 
 CASE(multi_head_attention_bf16_prefill_and_one_row) {
-    // head dim 128 (prefill and one-row kernels) and 64 (the prefill kernel's other layout)
+    // head dim 128 (prefill and one-row kernels) and 64 (the prefill kernel's other
+    // layout); the registered sliding_window_attention's window, and a window with ALiBi
     const DType dt = DType::BFloat16;
-    struct Shape { int64_t sq, sk, h, kvh, d; bool causal; };
-    for (Shape s : {Shape{256, 256, 8, 2, 128, true}, Shape{1, 700, 32, 8, 128, true},
-                    Shape{96, 160, 4, 4, 128, false}, Shape{300, 300, 8, 8, 64, true}}) {
+    struct Shape { int64_t sq, sk, h, kvh, d; bool causal; int64_t window; float alibi; };
+    for (Shape s : {Shape{256, 256, 8, 2, 128, true, 0, 0.0f}, Shape{1, 700, 32, 8, 128, true, 0, 0.0f},
+                    Shape{96, 160, 4, 4, 128, false, 0, 0.0f}, Shape{300, 300, 8, 8, 64, true, 0, 0.0f},
+                    Shape{512, 512, 8, 2, 64, true, 128, 0.0f}, Shape{200, 330, 4, 2, 128, true, 50, 0.25f}}) {
         const int64_t d = s.d;
         auto q = encode(normal(81, s.sq * s.h * d, 0.0f, 0.3f), dt);
         auto k = encode(normal(82, s.sk * s.kvh * d, 0.0f, 0.3f), dt), v = encode(normal(83, s.sk * s.kvh * d), dt);
@@ -217,8 +219,10 @@ CASE(multi_head_attention_bf16_prefill_and_one_row) {
         cfg.HeadDim = d;
         cfg.Causal = s.causal;
         cfg.KVHeadCount = s.kvh;
+        cfg.WindowSize = s.window;
+        cfg.ALiBiSlope = s.alibi;
         be().MultiHeadAttention(cfg, dq.data, dk.data, dv.data, dout.data, s.sq, s.sk, dt);
-        or_mha_config oc{s.h, d, s.causal ? 1 : 0, 0, 0.0f, s.kvh};
+        or_mha_config oc{s.h, d, s.causal ? 1 : 0, s.window, s.alibi, s.kvh};
         std::vector<uint8_t> ref(q.size());
         EXPECT(or_mha(&oc, q.data(), k.data(), v.data(), ref.data(), s.sq, s.sk, static_cast<int>(dt)) == 0, "oracle");
         const double e = normwise(download_f32(dout, dt), decode(ref, dt, s.sq * s.h * d));
