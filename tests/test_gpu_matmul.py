@@ -51,13 +51,14 @@ def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("rows,inner,cols", [(64, 4096, 4096), (1, 4104, 2056), (200, 1000, 1024),
-                                             (256, 512, 14336), (3, 64, 8), (500, 1032, 4104)])
+                                             (256, 512, 14336), (3, 64, 8), (500, 1032, 4104), (256, 512, 1024)])
 def test_matmul_16bit_skinny_split_k(backend, dt, rows, inner, cols):
     """rows <= 512 take the split-K kernel (64 x 128 tiles over chunks of K, f32
     partials summed in chunk order): ragged rows / columns, K tails, one-chunk and
     many-chunk splits; 200 x 1000 x 1024 (128 to 256 rows, a right operand of at
     most 2^22 elements) takes the small kernel instead, K split over the 8 waves of
-    each block, as do 256x256x128 and 128x512x512 above.  Oracle rows sampled across the tile bands (all columns),
+    each block, on 16 x 16 tiles (as do 256x256x128 and 128x512x512 above), and
+    256 x 512 x 1024 (256 tiles of 32 x 32) on 32 x 32 tiles.  Oracle rows sampled across the tile bands (all columns),
     numpy's f64 product for the whole output, and two calls bit-identical."""
     a = O.from_f32(seeded(rows * 3 + inner, (rows, inner)), dt)
     b = O.from_f32(seeded(cols * 7 + inner, (inner, cols), 0.0, 0.05), dt)
@@ -190,11 +191,13 @@ def test_matmul_f64_and_f32(backend):
 
 
 @pytest.mark.parametrize("rows,inner,cols", [(128, 512, 512), (100, 1000, 300), (64, 96, 48), (7, 13, 5),
-                                             (300, 40, 1100), (200, 333, 250), (32, 8192, 1024)])
+                                             (300, 40, 1100), (200, 333, 250), (32, 8192, 1024),
+                                             (256, 1024, 1024)])
 def test_matmul_f32_split_k(backend, rows, inner, cols):
     """F32 (config 1's Matmul): small outputs of moderate depth (at least 32 32x32
     tiles and few 64-deep steps per wave: 128x512x512, 100x1000x300, 200x333x250
-    with unaligned A rows) split K across the 8 waves of a block on the f32 MFMA;
+    with unaligned A rows on 16 x 16 tiles, 256x1024x1024 on 32 x 32 tiles) split
+    K across the 8 waves of a block on the f32 MFMA;
     other grids of fewer than 256 64x64 tiles (64x96x48, 32x8192x1024: too deep
     for its 32 tiles) split K across blocks into 16-deep-step chunks summed in
     order; ragged shapes and K tails, against the oracle's index-order f32 sum
