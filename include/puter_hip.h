@@ -19,10 +19,11 @@
  *     makes itself is a split-K scratch shared by puter_hip_matmul (16-bit
  *     formats with at most 512 rows, F32 outputs of fewer than 256 64x64 tiles,
  *     when K is split across blocks rather than inside them) and
- *     puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16 / f16,
- *     head dim 128, no ALiBi): one buffer per device, allocated on first use and
- *     grown on demand (Matmul: at most ~16 MB; one-row attention: the paged
- *     decode workspace size).  A growth is stream-ordered on the calling
+ *     puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16 / f16 at
+ *     head dim 128 without ALiBi, or any row over more than 768 keys): one buffer
+ *     per device, allocated on first use and grown on demand (Matmul: at most
+ *     ~16 MB; one-row attention: the paged decode workspace size, or
+ *     batch x heads x ceil(seq_k / 256) x (head_dim + 2) floats).  A growth is stream-ordered on the calling
  *     stream (hipFreeAsync of the old buffer after its last user, then
  *     hipMallocAsync): it never blocks the host.
  *

@@ -15,6 +15,10 @@ struct MhaArgs {
     float alibi;
     float scale;
     int64_t shift;  // causal: key k is visible to query row q iff k <= q + shift
+    // one-row split of the general kernel: per (batch, head, split) the chunk's
+    // (max, sum) and unnormalised output row; null otherwise
+    float2 *part_ml = nullptr;
+    float *part_o = nullptr;
 };
 
 // MFMA flash prefill (prefill.hip).  Returns true and sets *status when the

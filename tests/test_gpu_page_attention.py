@@ -280,6 +280,35 @@ def test_mha_one_query_row(backend, dt, b, sk, h, kvh, causal, window):
         assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"one-row mha sequence {i}")
 
 
+@pytest.mark.parametrize("dt,d,b,sk,h,kvh,causal,window,alibi", [
+    (O.BF16, 64, 1, 4096, 8, 2, True, 0, 0.0),      # the registered 8 x 64 heads at a decode step
+    (O.BF16, 64, 3, 769, 8, 8, True, 128, 0.0),     # four chunks, the last of one key; window
+    (O.F16, 48, 2, 1000, 4, 2, False, 0, 0.0),      # odd head dim, f16 dots
+    (O.F32, 64, 1, 800, 8, 8, True, 0, 0.0),        # f32 (config 1's format)
+    (O.BF16, 128, 2, 900, 8, 2, True, 0, 0.25),     # head dim 128 with ALiBi (not the decode kernels)
+    (O.F32, 256, 1, 1100, 2, 1, True, 0, -0.5),     # widest head dim
+    (O.BF16, 64, 2, 512, 8, 2, True, 0, 0.0),       # two chunks: the unsplit kernel
+])
+def test_mha_one_query_row_split(backend, dt, d, b, sk, h, kvh, causal, window, alibi):
+    """seqQ = 1 outside the decode kernels' shapes, over more than 768 keys: the
+    general kernel split over 256-key chunks, merged in order, against the oracle
+    per sequence (the last case stays unsplit)."""
+    import puter_amd
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(710 + sk, (b, 1, h * d), 0.0, std), dt)
+    k = encode(seeded(711 + sk, (b, sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(712 + sk, (b, sk, kvh * d)), dt)
+    out = empty_dev((b, 1, h * d), NP[dt])
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, window, alibi, kvh)
+    backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, 1, sk, dt)
+    got = decode(to_host(out, NP[dt]), dt)
+    for i in range(b):
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, window=window, alibi=alibi,
+                           dtype=dt), dt)
+        assert_close(got[i], ref, TOL[dt], elem_tol=1e-3 if dt == O.F32 else None,
+                     what=f"split one-row mha sequence {i}")
+
+
 def test_mha_one_query_row_unaligned_falls_back(backend):
     """A query not 16-byte aligned (an odd element offset) cannot take the decode
     kernels' 16-byte loads: the call falls back to the general kernel and the
