@@ -528,8 +528,9 @@ CASE(kv_page_write_fp8_and_dequant4) {
 CASE(host_threads_with_their_own_streams) {
     // The shim must be thread-safe (one context, a stream per backend): four host
     // threads, each with its own stream and Backend, run the split-K Matmul and
-    // one-row MultiHeadAttention (both lease the library's shared split-K scratch,
-    // ordered across streams by its completion event) and RMSNorm, 12 rounds each,
+    // one-row MultiHeadAttention at head dim 128 (the decode kernels) and 64 (the
+    // general kernel split over key chunks) (all three lease the library's shared
+    // split-K scratch, ordered across streams by its completion event) and RMSNorm, 12 rounds each,
     // all at once; every result equals the single-threaded one.  The scratch is
     // grown to its final size by the single-threaded pass first, so the threads
     // only share it.
@@ -547,13 +548,19 @@ CASE(host_threads_with_their_own_streams) {
     mha.HeadDim = D;
     mha.Causal = true;
     mha.KVHeadCount = KVH;
+    MultiHeadAttentionConfig mha64 = mha;   // the same buffers as 64 heads of 64 over 16 kv heads
+    mha64.NumHeads = 2 * H;
+    mha64.HeadDim = D / 2;
+    mha64.KVHeadCount = 2 * KVH;
     RMSNormConfig rc;
     rc.Epsilon = 1e-5;
     Tensor rmm = be().AllocateTensor({M, N}, bf), rat = be().AllocateTensor({1, H * D}, bf), rno = be().AllocateTensor({R, HID}, bf);
     be().Matmul(rmm.data, da.data, db.data, M, K, N, bf);
     be().MultiHeadAttention(mha, dq.data, dk.data, dv.data, rat.data, 1, SK, bf);
+    Tensor r64 = be().AllocateTensor({1, H * D}, bf);
+    be().MultiHeadAttention(mha64, dq.data, dk.data, dv.data, r64.data, 1, SK, bf);
     be().RMSNorm(rc, dx.data, dg.data, rno.data, R, HID, bf);
-    const auto want_mm = download(rmm), want_at = download(rat), want_no = download(rno);
+    const auto want_mm = download(rmm), want_at = download(rat), want_no = download(rno), want_64 = download(r64);
     constexpr int T = 4, ROUNDS = 12;
     std::atomic<int> failures{0};
     std::vector<std::string> why(T);
@@ -565,11 +572,12 @@ CASE(host_threads_with_their_own_streams) {
                 Check(puter_hip_stream_create(&stream));
                 Backend mine(stream);
                 Tensor omm = mine.AllocateTensor({M, N}, bf), oat = mine.AllocateTensor({1, H * D}, bf);
-                Tensor ono = mine.AllocateTensor({R, HID}, bf);
+                Tensor ono = mine.AllocateTensor({R, HID}, bf), o64 = mine.AllocateTensor({1, H * D}, bf);
                 std::vector<uint8_t> got;
                 for (int round = 0; round < ROUNDS; ++round) {
                     mine.Matmul(omm.data, da.data, db.data, M, K, N, bf);
                     mine.MultiHeadAttention(mha, dq.data, dk.data, dv.data, oat.data, 1, SK, bf);
+                    mine.MultiHeadAttention(mha64, dq.data, dk.data, dv.data, o64.data, 1, SK, bf);
                     mine.RMSNorm(rc, dx.data, dg.data, ono.data, R, HID, bf);
                     got.resize(want_mm.size());
                     mine.Download(got.data(), omm.data, got.size());
@@ -577,6 +585,9 @@ CASE(host_threads_with_their_own_streams) {
                     got.resize(want_at.size());
                     mine.Download(got.data(), oat.data, got.size());
                     if (got != want_at) throw std::runtime_error("attention differs in round " + std::to_string(round));
+                    got.resize(want_64.size());
+                    mine.Download(got.data(), o64.data, got.size());
+                    if (got != want_64) throw std::runtime_error("head-dim-64 attention differs in round " + std::to_string(round));
                     got.resize(want_no.size());
                     mine.Download(got.data(), ono.data, got.size());
                     if (got != want_no) throw std::runtime_error("RMSNorm differs in round " + std::to_string(round));
