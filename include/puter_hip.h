@@ -321,7 +321,7 @@ PUTER_API int puter_hip_flash_attention(const puter_flash_config *config, const 
  * K/V pools [pages, page_size, Hkv, D] of kv_dtype: BF16 or F16 (query and
  * output [batch, Hq*D] in the same format), or F8E4M3 with fp32 k_scale/v_scale
  * per kv head, value = decode(byte) * scale (query and output bf16);
- * D = 128, Hq/Hkv in {1, 2, 4, 8}; page_table [batch, max_pages_per_seq] int32;
+ * D = 128, Hq/Hkv from 1 to 16; page_table [batch, max_pages_per_seq] int32;
  * context_lens [batch] int32 (clamped to max_context); num_pages = pool size:
  * a token whose page id is outside [0, num_pages) is masked, never read.
  * workspace: caller-owned device buffer of

@@ -83,9 +83,13 @@ __device__ __forceinline__ uint4 fp8x8_to_bf16(uint2 raw) {
 // against a one-wave-per-split walk over 32-token sub-chunks:
 // bf16 +1%, fp8 +4%; MFMA P.V with 16-byte fp8 row pieces then took fp8 from
 // 144.6 to 138.0 us (bf16 unchanged).
-template <int KV, int G, bool O32>
+// GT: the query heads per kv head (1, 2, 4 or 8), or 0 for any other count up to
+// 16, read from the arguments (the score and P.V MFMAs are 16 heads wide either
+// way; the heads past the group are zero).
+template <int KV, int GT, bool O32>
 __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     constexpr int D = 128, TW = 64;
+    const int G = GT ? GT : (int)(a.heads / a.kv_heads);
     constexpr bool BF = KV == PUTER_BF16;
     constexpr bool H16 = KV == PUTER_F16;   // f16 pools, query and output
     constexpr bool W16 = BF || H16;          // 16-bit K/V rows (else fp8)
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     // per-wave 32-row tiles: K rows (256 bytes 16-bit, 128 fp8), then V rows (fp8
     // widened to bf16: 256 bytes), then the o merge
     __shared__ __attribute__((aligned(1024))) char k_lds[4][32 * 256];
-    __shared__ float ml_lds[4][G][2];
+    __shared__ float ml_lds[4][GT ? GT : 16][2];
 
     // Block order.  Consecutive dispatch ids go round-robin over the 8 XCDs; XCD x
     // runs a group of gk kv heads of chunk (split, sequence) 8n + x one after
@@ -454,7 +458,7 @@ bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *s
     if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || m.dim != 128 || m.seq_q != 1 || m.alibi != 0.0f)
         return false;
     const int64_t G = m.heads / m.kv_heads;
-    if (G != 1 && G != 2 && G != 4 && G != 8) return false;
+    if (G < 1 || G > 16) return false;
     if (!aligned16(m.q) || !aligned16(m.k) || !aligned16(m.v) || !aligned16(m.o)) return false;
     if (m.batch > 65535 || m.seq_k > 0x7FFFFFFF / std::max<int64_t>(m.batch, 1) || m.kv_heads > 0x7FFFFFFF)
         return false;
@@ -480,6 +484,7 @@ bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *s
     case 2: decode_block_kernel<KVD, 2, O><<<grid, 256, 0, s>>>(a); break;             \
     case 4: decode_block_kernel<KVD, 4, O><<<grid, 256, 0, s>>>(a); break;             \
     case 8: decode_block_kernel<KVD, 8, O><<<grid, 256, 0, s>>>(a); break;             \
+    default: decode_block_kernel<KVD, 0, O><<<grid, 256, 0, s>>>(a); break;            \
     }
 #define PUTER_ONE_ROW(KVD)                                                             \
     if (o32) { PUTER_ONE_ROW_G(KVD, true) }                                            \
@@ -520,7 +525,7 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     if (head_dim != 128) return fail(PUTER_ERR_INVALID, "paged decode: head_dim %lld unsupported (128)", (long long)head_dim);
     if (num_heads % kv_heads != 0) return fail(PUTER_ERR_INVALID, "paged decode: heads not divisible by kv heads");
     const int64_t G = num_heads / kv_heads;
-    if (G != 1 && G != 2 && G != 4 && G != 8) return fail(PUTER_ERR_INVALID, "paged decode: group size %lld unsupported", (long long)G);
+    if (G < 1 || G > 16) return fail(PUTER_ERR_INVALID, "paged decode: group size %lld unsupported (at most 16 query heads per kv head)", (long long)G);
     if (kv_dtype != PUTER_BF16 && kv_dtype != PUTER_F16 && kv_dtype != PUTER_F8E4M3)
         return fail(PUTER_ERR_INVALID, "paged decode: kv dtype %d unsupported", kv_dtype);
     if (num_pages > 0 && (num_pages > 0x7FFFFFFF / page_size || max_pages_per_seq > 0x7FFFFFFF / page_size))
@@ -560,6 +565,7 @@ int puter_hip_paged_decode_attention(const void *query, const void *key_pages,
     case 2: decode_block_kernel<KV, 2, O><<<grid, 256, 0, s>>>(a); break;             \
     case 4: decode_block_kernel<KV, 4, O><<<grid, 256, 0, s>>>(a); break;             \
     case 8: decode_block_kernel<KV, 8, O><<<grid, 256, 0, s>>>(a); break;             \
+    default: decode_block_kernel<KV, 0, O><<<grid, 256, 0, s>>>(a); break;            \
     }
 #define PUTER_DECODE(KV)                                                              \
     if (o32) { PUTER_DECODE_G(KV, true) }                                             \

@@ -256,6 +256,7 @@ def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
     (3, 700, 8, 4, True, 0),       # batched, partial last split
     (64, 2000, 32, 8, True, 0),    # 256-token splits (enough waves)
     (2, 900, 16, 4, True, 128),    # sliding_window_attention's window: hides no key of row 0
+    (2, 1000, 28, 4, True, 0),     # group size 7 (read at run time)
 ])
 def test_mha_one_query_row(backend, dt, b, sk, h, kvh, causal, window):
     """seqQ = 1 (the reference's decode step after KVPageGather) runs on the paged
@@ -624,11 +625,13 @@ def test_paged_decode_fp8_value_codes_exact(backend):
     assert np.array_equal(got[~nan], want[~nan])   # -0 sums to +0, as the reference's 0 + 1 * v does
 
 
-# group sizes 1, 2, 4, 8; kv head counts 1, 2, 3, 4, 8 (the XCD grouping of kv heads
-# falls back to smaller groups, down to one, when it does not divide them); page
-# sizes that do not divide a wave's 64 tokens
+# group sizes 1, 2, 4, 8 (compiled in) and 3, 5, 7, 16 (read at run time); kv head
+# counts 1, 2, 3, 4, 8 (the XCD grouping of kv heads falls back to smaller groups,
+# down to one, when it does not divide them); page sizes that do not divide a
+# wave's 64 tokens
 @pytest.mark.parametrize("kv_dt", [O.BF16, O.F16, O.F8E4M3])
-@pytest.mark.parametrize("h,kvh", [(8, 8), (8, 4), (16, 2), (4, 1), (6, 3)])
+@pytest.mark.parametrize("h,kvh", [(8, 8), (8, 4), (16, 2), (4, 1), (6, 3), (32, 2), (7, 1), (15, 3),
+                                   (12, 4)])
 @pytest.mark.parametrize("ps,lo,hi", [(1, 1, 70), (5, 30, 300), (32, 200, 700)])
 def test_paged_decode_groups_pages(backend, kv_dt, h, kvh, ps, lo, hi):
     d, batch = 128, 3
