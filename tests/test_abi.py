@@ -117,6 +117,9 @@ def test_attention_validation(lib):
     bad[12] = 65                                                    # max_context > pages*page_size
     assert lib.puter_hip_paged_decode_attention(*bad) == _lib.ERR_INVALID
     bad = list(args)
+    bad[9], bad[10] = 34, 2                                         # 17 query heads per kv head (at most 16)
+    assert lib.puter_hip_paged_decode_attention(*bad) == _lib.ERR_INVALID
+    bad = list(args)
     bad[15] = 3                                                     # fp8 without scales
     assert lib.puter_hip_paged_decode_attention(*bad) == _lib.ERR_NIL
     # Matmul takes F32 / F64 / BF16 / F16 (compute.go:46-62); fp8 is rejected
