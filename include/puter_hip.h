@@ -25,7 +25,14 @@
  *     ~16 MB; one-row attention: the paged decode workspace size, or
  *     batch x heads x ceil(seq_k / 256) x (head_dim + 2) floats).  A growth is stream-ordered on the calling
  *     stream (hipFreeAsync of the old buffer after its last user, then
- *     hipMallocAsync): it never blocks the host.
+ *     hipMallocAsync): it never blocks the host.  On a stream that is capturing
+ *     a HIP graph these calls allocate, free, wait on and record nothing: they
+ *     use the buffer held if it is large enough (the graph keeps its address,
+ *     so that buffer is never freed: a later growth keeps it and allocates
+ *     beside it) and otherwise return PUTER_ERR_INVALID before launching; make
+ *     the same call, or a larger one, outside the capture first.  Replays share
+ *     the buffer with eager scratch-using calls until such a growth, so the
+ *     caller orders them (one stream, or its own events).
  *
  * Status codes follow the reference's CUDA bridge (device/cuda/internal/bridge/status.c):
  *   -2 nil buffer, -6 invalid dtype / shape / config, -7 device unavailable,
@@ -195,8 +202,9 @@ enum puter_gate_kind {
     PUTER_GATE_GLU = 4,        /* gate * sigmoid(up) */
     PUTER_GATE_REGLU = 5,      /* gate * relu(up) */
     PUTER_GATE_LINGLU = 6,     /* gate * up */
+    PUTER_GATE_SEGLU = 7,      /* up * sigmoid(gate)   (FastSeGLU32, math/extra_activation.go:88-90) */
 };
-/* <Kind>Tensors(dst, gate, up, count, format): interface.go:28,35,52,62 ...
+/* <Kind>Tensors(dst, gate, up, count, format): interface.go:28,35,52,57,62 ...
  * device/cpu/activation/gated.go:59-136 */
 PUTER_API int puter_hip_gated_tensors(int kind, void *dst, const void *gate, const void *up,
                             int64_t count, int dtype, void *stream);

@@ -16,7 +16,8 @@ import numpy as np
 from .build import LIBRARY, build
 
 F32, F16, BF16, F8E4M3, F8E5M2, I32, I8, I4, F64 = 0, 1, 2, 3, 4, 5, 6, 7, 8
-GATE_SWIGLU, GATE_GEGLU, GATE_GEGLU_TANH, GATE_SIGLU, GATE_GLU, GATE_REGLU, GATE_LINGLU = range(7)
+(GATE_SWIGLU, GATE_GEGLU, GATE_GEGLU_TANH, GATE_SIGLU, GATE_GLU, GATE_REGLU, GATE_LINGLU,
+ GATE_SEGLU) = range(8)
 UNARY_SILU, UNARY_GELU = 0, 1
 
 _lib = None

@@ -68,6 +68,7 @@ static float combine(int kind, float g, float u) {
     case OR_GATE_GLU: return g * sigmoid32(u);            /* FastGLU32 activation.go:286-288 */
     case OR_GATE_REGLU: return g * (u > 0 ? u : 0);       /* FastReGLU32 activation.go:298-300 */
     case OR_GATE_LINGLU: return g * u;                    /* FastLinGLU32 extra_activation.go:84-86 */
+    case OR_GATE_SEGLU: return u * sigmoid32(g);          /* FastSeGLU32 extra_activation.go:88-90 */
     default: return NAN;
     }
 }
@@ -77,7 +78,7 @@ static int gated_dtype_ok(int dtype) { return dtype == OR_F32 || dtype == OR_F16
 int or_gated_tensors(int kind, void *dst, const void *gate, const void *up,
                      int64_t count, int dtype) {
     if (count == 0) return 0;
-    if (!gated_dtype_ok(dtype) || kind < 0 || kind > OR_GATE_LINGLU) return -6;
+    if (!gated_dtype_ok(dtype) || kind < 0 || kind > OR_GATE_SEGLU) return -6;
 #pragma omp parallel for schedule(static) num_threads(oracle_get_threads())
     for (int64_t i = 0; i < count; ++i)
         or_store(dst, (size_t)i, combine(kind, or_load(gate, (size_t)i, dtype),
@@ -89,7 +90,7 @@ int or_gated_tensors(int kind, void *dst, const void *gate, const void *up,
 int or_gated_packed(int kind, void *dst, const void *packed,
                     int64_t batch, int64_t half_count, int dtype) {
     if (batch == 0 || half_count == 0) return 0;
-    if (!gated_dtype_ok(dtype) || kind < 0 || kind > OR_GATE_LINGLU) return -6;
+    if (!gated_dtype_ok(dtype) || kind < 0 || kind > OR_GATE_SEGLU) return -6;
 #pragma omp parallel for schedule(static) num_threads(oracle_get_threads())
     for (int64_t b = 0; b < batch; ++b) {
         size_t row = (size_t)(b * half_count * 2), out = (size_t)(b * half_count);

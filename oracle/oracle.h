@@ -21,6 +21,11 @@
  *     manifesto/dtype boundary, see header of numeric.c).
  *   - norms/rope/activations/attention: reference known-answer tests, closed
  *     forms, and f64 brute force on tiny shapes.
+ *   - every gate kind (ReGLU / LinGLU / SeGLU included), the fp8 paged-decode
+ *     branch (torch's E4M3 decode, distinct per-head K and V scales), Matmul in
+ *     F32 / F64 / BF16 / F16 (exact sums, single-rounding sums) and the f16
+ *     attention dot rounding each have a check that does not restate their
+ *     formula (tests/test_oracle_pins_glu_decode_matmul.py).
  */
 #ifndef PUTER_ORACLE_H
 #define PUTER_ORACLE_H
@@ -123,7 +128,7 @@ int or_rope_pairs(float *output, const float *input, const float *cos_buffer, co
 
 /* ---- activation.c ---- */
 enum { OR_GATE_SWIGLU = 0, OR_GATE_GEGLU = 1, OR_GATE_GEGLU_TANH = 2, OR_GATE_SIGLU = 3,
-       OR_GATE_GLU = 4, OR_GATE_REGLU = 5, OR_GATE_LINGLU = 6 };
+       OR_GATE_GLU = 4, OR_GATE_REGLU = 5, OR_GATE_LINGLU = 6, OR_GATE_SEGLU = 7 };
 int or_gated_tensors(int kind, void *dst, const void *gate, const void *up,
                      int64_t count, int dtype);
 int or_gated_packed(int kind, void *dst, const void *packed,

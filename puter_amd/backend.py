@@ -15,7 +15,8 @@ from . import _lib
 from ._lib import check, PuterError  # noqa: F401
 
 F32, F16, BF16, F8E4M3, F8E5M2, I32, I8, I4, F64 = 0, 1, 2, 3, 4, 5, 6, 7, 8
-GATE_SWIGLU, GATE_GEGLU, GATE_GEGLU_TANH, GATE_SIGLU, GATE_GLU, GATE_REGLU, GATE_LINGLU = range(7)
+(GATE_SWIGLU, GATE_GEGLU, GATE_GEGLU_TANH, GATE_SIGLU, GATE_GLU, GATE_REGLU, GATE_LINGLU,
+ GATE_SEGLU) = range(8)
 UNARY_SILU, UNARY_GELU = 0, 1
 
 ErrLenMismatch = "convert: length mismatch"  # convert/errors.go:10-15
@@ -131,11 +132,14 @@ class Backend:
         self.lib = _lib.load()
         self._stream = stream
         self._status = None   # device int32 status word of the paged-KV hooks
+        import torch
+        if torch.cuda.is_available():
+            self._status_word()   # made here, so no hook call allocates (graph capture)
 
     def _status_word(self):
         """The backend's device status word (the Go wrapper keeps one per backend):
         the paged-KV hooks store PUTER_ERR_INVALID into it when a page id or slot
-        is out of range."""
+        is out of range.  The constructor makes it when a GPU is present."""
         if self._status is None:
             import torch
             self._status = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -302,6 +306,9 @@ class Backend:
     def LinGLUTensors(self, dst, gate, up, count, format):
         self._tensors(GATE_LINGLU, dst, gate, up, count, format)
 
+    def SeGLUTensors(self, dst, gate, up, count, format):
+        self._tensors(GATE_SEGLU, dst, gate, up, count, format)
+
     def SwiGLU(self, dst, packed, batch, halfCount, format):
         self._packed(GATE_SWIGLU, dst, packed, batch, halfCount, format)
 
@@ -322,6 +329,9 @@ class Backend:
 
     def LinGLU(self, dst, packed, batch, halfCount, format):
         self._packed(GATE_LINGLU, dst, packed, batch, halfCount, format)
+
+    def SeGLU(self, dst, packed, batch, halfCount, format):
+        self._packed(GATE_SEGLU, dst, packed, batch, halfCount, format)
 
     def Silu(self, dst, src, count, format):
         check(self.lib.puter_hip_unary(UNARY_SILU, _ptr(dst), _ptr(src), count, format,

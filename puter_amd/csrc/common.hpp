@@ -23,7 +23,10 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 // and of one-row attention), held for one call's launches: the constructor orders
 // the call's stream after the buffer's last user on another stream and grows the
 // buffer if needed; finish() records the call's completion on its stream.  The
-// device's lock is held from construction to destruction.
+// device's lock is held from construction to destruction.  On a stream that is
+// capturing a graph the lease neither grows, orders nor records: it hands out the
+// buffer it finds (never freed afterwards) or fails with PUTER_ERR_INVALID when
+// that is too small.
 struct SplitScratch;
 class ScratchLease {
 public:
@@ -39,6 +42,7 @@ private:
     hipStream_t s_;
     void *ptr_ = nullptr;
     int status_ = 0;
+    bool captured_ = false;
 };
 
 inline bool is_float_dtype(int dt) { return dt >= PUTER_F32 && dt <= PUTER_F8E5M2; }

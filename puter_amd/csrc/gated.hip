@@ -1,4 +1,4 @@
-// Gated activations (SwiGLU, GeGLU, GeGLUTanh, SiGLU, GLU, ReGLU, LinGLU) in
+// Gated activations (SwiGLU, GeGLU, GeGLUTanh, SiGLU, GLU, ReGLU, LinGLU, SeGLU) in
 // tensor form and packed form, plus unary Silu / Gelu.
 // Reference: device/cpu/activation/gated.go:10-136, compute.go:72-176 and the
 // scalar math of device/cpu/math/f32.go:21-105, math/activation.go:26-57,286-308.
@@ -71,6 +71,7 @@ __device__ __forceinline__ float combine(float g, float u) {
     else if constexpr (KIND == PUTER_GATE_SIGLU) return __fmul_rn(sigmoid32(g), u);
     else if constexpr (KIND == PUTER_GATE_GLU) return __fmul_rn(g, sigmoid32(u));
     else if constexpr (KIND == PUTER_GATE_REGLU) return __fmul_rn(g, u > 0 ? u : 0.0f);
+    else if constexpr (KIND == PUTER_GATE_SEGLU) return __fmul_rn(u, sigmoid32(g));
     else return __fmul_rn(g, u);
 }
 
@@ -192,6 +193,7 @@ static int gated_by_kind(int kind, bool packed, void *dst, const void *a, const 
         PUTER_GATE_CASE(PUTER_GATE_GLU)
         PUTER_GATE_CASE(PUTER_GATE_REGLU)
         PUTER_GATE_CASE(PUTER_GATE_LINGLU)
+        PUTER_GATE_CASE(PUTER_GATE_SEGLU)
     default: return fail(PUTER_ERR_INVALID, "gated: unknown kind %d", kind);
     }
 #undef PUTER_GATE_CASE

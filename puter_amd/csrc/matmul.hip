@@ -46,6 +46,7 @@
 #include <cstdint>
 #include <mutex>
 #include <type_traits>
+#include <vector>
 
 namespace puter {
 
@@ -685,6 +686,15 @@ __global__ __launch_bounds__(256) void matmul_splitk_reduce_kernel(uint16_t *c, 
 // one in stream order on the calling stream (hipFreeAsync / hipMallocAsync),
 // after the last user's work.  The mutex is held from acquisition until the
 // call's launches and event are enqueued.
+//
+// Under stream capture (a HIP graph being recorded) a call allocates, frees,
+// waits on and records nothing: it uses the buffer it finds when that is large
+// enough and otherwise fails with PUTER_ERR_INVALID before any launch.  The
+// graph keeps the buffer's address, so a buffer a capture has used is never
+// freed: a later growth retires it (kept until the process ends) and allocates
+// the new one beside it.  Replays of such a graph share the buffer with eager
+// calls until that growth; the caller orders them (one stream, or its own
+// events), as it orders any two uses of one buffer.
 struct SplitScratch {
     std::mutex mu;
     void *ptr = nullptr;
@@ -692,8 +702,20 @@ struct SplitScratch {
     hipEvent_t done = nullptr;  // recorded after the last call that used ptr
     hipStream_t last = nullptr;
     bool used = false;
+    bool pinned = false;        // a captured graph holds ptr
+    std::vector<void *> retired;  // pinned buffers replaced by a growth
 };
 static SplitScratch g_split_scratch[64];
+
+// Whether s is recording a graph (an invalidated capture counts: it must not
+// allocate either).
+static int stream_capturing(hipStream_t s, bool *capturing) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess)
+        return fail(PUTER_ERR_LAUNCH, "scratch: cannot query the stream's capture status");
+    *capturing = st != hipStreamCaptureStatusNone;
+    return PUTER_OK;
+}
 
 static int scratch_acquire(SplitScratch &sc, size_t need, hipStream_t s) {
     if (!sc.done && hipEventCreateWithFlags(&sc.done, hipEventDisableTiming) != hipSuccess)
@@ -701,7 +723,12 @@ static int scratch_acquire(SplitScratch &sc, size_t need, hipStream_t s) {
     if (sc.used && sc.last != s && hipStreamWaitEvent(s, sc.done, 0) != hipSuccess)
         return fail(PUTER_ERR_LAUNCH, "matmul: cannot order the split-K scratch");
     if (sc.bytes < need) {
-        if (sc.ptr) {
+        if (sc.ptr && sc.pinned) {
+            sc.retired.push_back(sc.ptr);  // a graph may still replay into it
+            sc.ptr = nullptr;
+            sc.bytes = 0;
+            sc.pinned = false;
+        } else if (sc.ptr) {
             // s is ordered after the last user (above, or it is that user)
             if (hipFreeAsync(sc.ptr, s) != hipSuccess)
                 return fail(PUTER_ERR_LAUNCH, "matmul: cannot release the split-K scratch");
@@ -726,12 +753,29 @@ ScratchLease::ScratchLease(size_t bytes, hipStream_t s) : s_(s) {
     }
     sc_ = &g_split_scratch[dev];
     lock_ = std::unique_lock<std::mutex>(sc_->mu);
+    bool capturing = false;
+    if ((status_ = stream_capturing(s, &capturing)) != PUTER_OK) return;
+    if (capturing) {
+        if (sc_->bytes < bytes) {
+            status_ = fail(PUTER_ERR_INVALID,
+                           "scratch: %zu bytes needed under stream capture, %zu held; the library's scratch "
+                           "cannot grow while a graph is captured (make the same call, or a larger one, "
+                           "outside the capture first)",
+                           bytes, sc_->bytes);
+            return;
+        }
+        sc_->pinned = true;
+        captured_ = true;
+        ptr_ = sc_->ptr;
+        return;
+    }
     status_ = scratch_acquire(*sc_, bytes, s);
     if (status_ == PUTER_OK) ptr_ = sc_->ptr;
 }
 
 int ScratchLease::finish() {
     if (status_ != PUTER_OK) return status_;
+    if (captured_) return PUTER_OK;
     if (hipEventRecord(sc_->done, s_) != hipSuccess) return fail(PUTER_ERR_LAUNCH, "scratch: cannot record the event");
     sc_->last = s_;
     sc_->used = true;

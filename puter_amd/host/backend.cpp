@@ -92,7 +92,13 @@ Tensor Wrap(void *data, std::vector<int64_t> shape, DType format, Location locat
 }
 
 // ---- backend ----------------------------------------------------------------------
-Backend::Backend(void *stream) : stream_(stream) {}
+// The paged-KV hooks' status word is made here, with a blocking upload of its
+// zero, so that no hook call (which may sit inside a HIP-graph capture) allocates
+// or synchronises; a host without a device makes it on first use instead.
+Backend::Backend(void *stream) : stream_(stream) {
+    int devices = 0;
+    if (puter_hip_device_count(&devices) == PUTER_OK && devices > 0) StatusWord();
+}
 
 Backend::~Backend() {
     if (status_) puter_hip_free(status_);
@@ -275,6 +281,7 @@ PUTER_TENSORS(SiGLUTensors, PUTER_GATE_SIGLU)
 PUTER_TENSORS(GLUTensors, PUTER_GATE_GLU)
 PUTER_TENSORS(ReGLUTensors, PUTER_GATE_REGLU)
 PUTER_TENSORS(LinGLUTensors, PUTER_GATE_LINGLU)
+PUTER_TENSORS(SeGLUTensors, PUTER_GATE_SEGLU)
 PUTER_PACKED(SwiGLU, PUTER_GATE_SWIGLU)
 PUTER_PACKED(GeGLU, PUTER_GATE_GEGLU)
 PUTER_PACKED(GeGLUTanh, PUTER_GATE_GEGLU_TANH)
@@ -282,6 +289,7 @@ PUTER_PACKED(SiGLU, PUTER_GATE_SIGLU)
 PUTER_PACKED(GLU, PUTER_GATE_GLU)
 PUTER_PACKED(ReGLU, PUTER_GATE_REGLU)
 PUTER_PACKED(LinGLU, PUTER_GATE_LINGLU)
+PUTER_PACKED(SeGLU, PUTER_GATE_SEGLU)
 #undef PUTER_TENSORS
 #undef PUTER_PACKED
 

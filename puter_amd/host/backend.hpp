@@ -167,8 +167,8 @@ public:
     // ErrShapeMismatch (device/cpu/shape/page.go:139-146,191-203) if a paged-KV
     // call since the last check saw an out-of-range page id or slot.
     void CheckStatus();
-    // The device int32 the paged-KV hooks flag bad ids in (created on first use;
-    // call once before capturing those hooks in a HIP graph).
+    // The device int32 the paged-KV hooks flag bad ids in (created by the
+    // constructor when a device is present, so the hooks can be captured).
     int32_t *StatusWord();
 
     // -- LayerNorm family: device/interface.go:355-379
@@ -212,6 +212,7 @@ public:
     void GLUTensors(void *dst, const void *gate, const void *up, int64_t count, DType format);
     void ReGLUTensors(void *dst, const void *gate, const void *up, int64_t count, DType format);
     void LinGLUTensors(void *dst, const void *gate, const void *up, int64_t count, DType format);
+    void SeGLUTensors(void *dst, const void *gate, const void *up, int64_t count, DType format);
     void SwiGLU(void *dst, const void *packed, int64_t batch, int64_t halfCount, DType format);
     void GeGLU(void *dst, const void *packed, int64_t batch, int64_t halfCount, DType format);
     void GeGLUTanh(void *dst, const void *packed, int64_t batch, int64_t halfCount, DType format);
@@ -219,6 +220,7 @@ public:
     void GLU(void *dst, const void *packed, int64_t batch, int64_t halfCount, DType format);
     void ReGLU(void *dst, const void *packed, int64_t batch, int64_t halfCount, DType format);
     void LinGLU(void *dst, const void *packed, int64_t batch, int64_t halfCount, DType format);
+    void SeGLU(void *dst, const void *packed, int64_t batch, int64_t halfCount, DType format);
     void Silu(void *dst, const void *src, int64_t count, DType format);
     void Gelu(void *dst, const void *src, int64_t count, DType format);
 

@@ -249,7 +249,8 @@ void RegisterHIPKernels(Registry &registry, Backend &be) {
     const std::pair<const char *, GatedMethod> gated_kinds[] = {
         {"swiglu", &Backend::SwiGLUTensors}, {"geglu", &Backend::GeGLUTensors},
         {"geglu_tanh", &Backend::GeGLUTanhTensors}, {"siglu", &Backend::SiGLUTensors},
-        {"glu", &Backend::GLUTensors}, {"reglu", &Backend::ReGLUTensors}, {"linglu", &Backend::LinGLUTensors}};
+        {"glu", &Backend::GLUTensors}, {"reglu", &Backend::ReGLUTensors}, {"linglu", &Backend::LinGLUTensors},
+        {"seglu", &Backend::SeGLUTensors}};
     for (D dt : {D::Float32, D::BFloat16, D::Float16}) {
         reg("layernorm", {dt, dt, dt}, {dt}, layernorm(be, dt));
         for (const auto &g : gated_kinds) reg(g.first, {dt, dt}, {dt}, gated(be, dt, g.second));

@@ -303,7 +303,7 @@ def _int8_quant(be):
 
 GATED = (("swiglu", "SwiGLUTensors"), ("geglu", "GeGLUTensors"), ("geglu_tanh", "GeGLUTanhTensors"),
          ("siglu", "SiGLUTensors"), ("glu", "GLUTensors"), ("reglu", "ReGLUTensors"),
-         ("linglu", "LinGLUTensors"))
+         ("linglu", "LinGLUTensors"), ("seglu", "SeGLUTensors"))
 
 
 def register_hip_kernels(registry: Registry = None, backend=None) -> Registry:

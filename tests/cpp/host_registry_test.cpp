@@ -65,13 +65,13 @@ CASE(hip_registrations) {
         EXPECT(k.Locations == std::vector<Location>{Location::Device}, "%s registered off the device", k.Name.c_str());
     }
     for (const char *n : {"page_write", "page_gather", "layernorm", "swiglu", "geglu", "geglu_tanh", "siglu", "glu",
-                          "reglu", "linglu", "silu", "gelu", "cast", "matmul", "multi_head_attention",
+                          "reglu", "linglu", "seglu", "silu", "gelu", "cast", "matmul", "multi_head_attention",
                           "grouped_query_attention", "sliding_window_attention", "attention", "flash_attention",
                           "int8_dequant", "int4_dequant", "int8_quant"})
         EXPECT(names.count(n), "%s not registered", n);
-    // page: 4 formats x 2; 3 formats x (layernorm + 7 gated + silu + gelu); matmul 4;
+    // page: 4 formats x 2; 3 formats x (layernorm + 8 gated + silu + gelu); matmul 4;
     // casts 6 x 5 float pairs + int8 <-> f32; attention 3 formats x 5; quantisation 3
-    EXPECT(r.Snapshot().size() == 8 + 30 + 4 + 32 + 15 + 3, "%zu kernels", r.Snapshot().size());
+    EXPECT(r.Snapshot().size() == 8 + 33 + 4 + 32 + 15 + 3, "%zu kernels", r.Snapshot().size());
     // the reference's own page signatures (slice_register.go:40-78) resolve to the
     // HIP kernels for device tensors, not for host ones
     for (DType dt : {DType::Float32, DType::BFloat16, DType::Float16}) {

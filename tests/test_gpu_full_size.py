@@ -116,8 +116,10 @@ def test_cast_f32_bf16_117m_round_trip(backend):
 
 
 def test_prefill_b4_s4096(backend):
-    """configs[3] (B4 S4096 Hq32 Hkv8 D128 causal bf16): the last batch's first,
-    middle and last 8 query rows of every head against the oracle."""
+    """configs[3] (B4 S4096 Hq32 Hkv8 D128 causal bf16): in every batch, three
+    groups of 8 query rows (a different set per batch: the first, a middle and the
+    last rows, and rows beside the 128-query block edges) of every head against
+    the oracle."""
     import torch
     import puter_amd
     B, S, H, KV, D = 4, 4096, 32, 8, 128
@@ -129,14 +131,15 @@ def test_prefill_b4_s4096(backend):
     o = torch.empty_like(q)
     backend.MultiHeadAttentionBatched(puter_amd.MultiHeadAttentionConfig(H, D, True, 0, 0.0, KV),
                                       q, k, v, o, B, S, S, O.BF16)
-    b = B - 1
-    host = lambda t, w: t.view(B, S * w)[b].cpu().view(torch.int16).numpy().view(np.uint16).reshape(S, w)  # noqa: E731
-    qh, kh, vh, oh = host(q, H * D), host(k, KV * D), host(v, KV * D), host(o, H * D)
     O.set_threads(8)
-    for lo in (0, S // 2, S - 8):
-        ref = O.mha_rows(qh, kh, vh, H, D, (0, H), (lo, lo + 8), kv_heads=KV, dtype=O.BF16)
-        assert_close(decode(oh[lo:lo + 8], O.BF16), decode(ref[lo:lo + 8], O.BF16), TOL[O.BF16],
-                     elem_tol=None, what=f"prefill rows {lo}..{lo + 7}")
+    rows = {0: (0, 1020, S - 8), 1: (124, S // 2, 3580), 2: (8, 2044, S - 132), 3: (0, S // 2, S - 8)}
+    for b in range(B):
+        host = lambda t, w: t.view(B, S * w)[b].cpu().view(torch.int16).numpy().view(np.uint16).reshape(S, w)  # noqa: E731
+        qh, kh, vh, oh = host(q, H * D), host(k, KV * D), host(v, KV * D), host(o, H * D)
+        for lo in rows[b]:
+            ref = O.mha_rows(qh, kh, vh, H, D, (0, H), (lo, lo + 8), kv_heads=KV, dtype=O.BF16)
+            assert_close(decode(oh[lo:lo + 8], O.BF16), decode(ref[lo:lo + 8], O.BF16), TOL[O.BF16],
+                         elem_tol=None, what=f"prefill batch {b} rows {lo}..{lo + 7}")
     del q, k, v, o
     torch.cuda.empty_cache()
 

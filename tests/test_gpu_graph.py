@@ -22,6 +22,7 @@ import pytest
 
 import oracle as O
 import puter_amd
+from puter_amd._lib import ERR_INVALID
 from helpers import TOL, assert_close, seeded, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
@@ -201,3 +202,120 @@ def test_prefill_block_graph_replays_match_eager(backend, head_dim):
         for name in ("h", "q", "k", "o", "r", "f", "y", "y32"):
             assert torch.equal(out_static[name], ref[name]), f"replay {step}: {name} differs from the eager block"
         (torch.randn(1 << 20, device="cuda") + 1).sum().item()   # eager work between replays
+
+
+def _one_row_inputs(dt, b, h, kvh, d, seq_k, seed):
+    q = encode_dt(seeded(seed, (b, h * d)), dt)
+    k = encode_dt(seeded(seed + 1, (b * seq_k, kvh * d), 0.0, 0.5), dt)
+    v = encode_dt(seeded(seed + 2, (b * seq_k, kvh * d)), dt)
+    return q, k, v
+
+
+def encode_dt(x, dt):
+    return x if dt == O.F32 else O.from_f32(x, dt)
+
+
+@pytest.mark.parametrize("dt,b,h,kvh,d,seq_k", [
+    (O.BF16, 1, 8, 8, 64, 1000),     # the registered 8 x 64 heads: general kernel split over 256-key chunks
+    (O.F32, 2, 4, 2, 64, 1500),      # f32, GQA: the same split path
+    (O.F16, 3, 16, 4, 128, 3000),    # f16 at head dim 128: the decode kernels over contiguous K/V
+])
+def test_one_row_mha_graph_uses_the_held_scratch(backend, dt, b, h, kvh, d, seq_k):
+    """One-row MultiHeadAttention (the reference's decode step after KVPageGather,
+    bind_router.go:640-684) keeps its split partials in the library's scratch.
+    Captured after an eager call of the same shape, the call reuses the held buffer
+    (no allocation, event wait or record inside the capture); three replays with
+    new inputs equal the eager calls bit for bit and the oracle to the dtype's
+    bar.  An eager call that then needs a larger scratch retires the captured
+    buffer instead of freeing it, and the graph still replays correctly."""
+    import torch
+
+    np_t = np.float32 if dt == O.F32 else np.uint16
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, True, 0, 0.0, kvh)
+    q0, k0, v0 = _one_row_inputs(dt, b, h, kvh, d, seq_k, 1100)
+    sq, sk, sv = to_dev(q0), to_dev(k0), to_dev(v0)
+    sout = torch.empty(sq.shape, dtype=sq.dtype, device="cuda")
+
+    def call(q, k, v, o):
+        backend.MultiHeadAttentionBatched(cfg, q, k, v, o, b, 1, seq_k, dt)
+
+    call(sq, sk, sv, sout)                      # eager warm-up: sizes the scratch
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(sq, sk, sv, sout)
+
+    def replay_and_check(step):
+        q, k, v = _one_row_inputs(dt, b, h, kvh, d, seq_k, 1110 + 10 * step)
+        ref = torch.empty_like(sout)
+        call(to_dev(q), to_dev(k), to_dev(v), ref)
+        torch.cuda.synchronize()
+        sq.copy_(to_dev(q)); sk.copy_(to_dev(k)); sv.copy_(to_dev(v))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(sout, ref), f"replay {step} differs from the eager call"
+        got = to_host(sout, np_t)
+        for bb in range(b):
+            want = O.mha(q[bb:bb + 1], k[bb * seq_k:(bb + 1) * seq_k], v[bb * seq_k:(bb + 1) * seq_k], h, d,
+                         causal=True, kv_heads=kvh, dtype=dt)
+            g, w = (got[bb:bb + 1], want) if dt == O.F32 else (O.to_f32(got[bb:bb + 1], dt), O.to_f32(want, dt))
+            assert_close(g, w, TOL[dt], elem_tol=None, what=f"replay {step} batch {bb}")
+        (torch.randn(1 << 20, device="cuda") * 3).sum().item()   # eager work between replays
+
+    for step in range(3):
+        replay_and_check(step)
+    # an eager call needing more scratch than the graph's buffer (135 MB of split
+    # partials: 2040 heads x 64 chunks x (8 + 4*256) bytes, f32 general path)
+    hh, dd, kk = 2040, 256, 64 * 256
+    big = puter_amd.MultiHeadAttentionConfig(hh, dd, True, 0, 0.0, 1)
+    bq = to_dev(seeded(1190, (1, hh * dd)))
+    bk = to_dev(seeded(1191, (kk, dd), 0.0, 0.5))
+    bo = torch.empty_like(bq)
+    backend.MultiHeadAttentionBatched(big, bq, bk, bk, bo, 1, 1, kk, O.F32)
+    torch.cuda.synchronize()
+    del bq, bk, bo
+    replay_and_check(3)
+
+
+def test_capture_that_would_grow_the_scratch_fails_before_launching(backend):
+    """A one-row MultiHeadAttention whose split partials exceed what the library's
+    scratch holds cannot be captured: the call raises PUTER_ERR_INVALID inside the
+    capture without allocating or launching (its output keeps the sentinel the
+    capture's own fill wrote), the capture ends normally, and the same call made
+    eagerly afterwards grows the scratch and matches the oracle on sampled heads."""
+    import torch
+
+    # 2040 heads x 256 chunks x (8 + 4*256) B = 539 MB of partials, more than
+    # any other call in this suite makes the scratch hold
+    b, h, kvh, d, seq_k = 1, 2040, 8, 256, 65536
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, True, 0, 0.0, kvh)
+    q = to_dev(O.from_f32(seeded(1200, (b, h * d)), O.BF16))
+    k = to_dev(O.from_f32(seeded(1201, (seq_k, kvh * d), 0.0, 0.5), O.BF16))
+    v = to_dev(O.from_f32(seeded(1202, (seq_k, kvh * d)), O.BF16))
+    out = torch.empty(q.shape, dtype=q.dtype, device="cuda")
+    marker = torch.empty(16, dtype=torch.float32, device="cuda")
+    err = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out.fill_(0x3F80)                      # bf16 1.0 everywhere
+        try:
+            backend.MultiHeadAttentionBatched(cfg, q, k, v, out, b, 1, seq_k, O.BF16)
+        except puter_amd.PuterError as e:
+            err = e
+        marker.fill_(2.0)
+    assert err is not None and err.status == ERR_INVALID, err
+    assert "capture" in str(err)
+    out.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert bool((out == 0x3F80).all()) and bool((marker == 2.0).all())
+    backend.MultiHeadAttentionBatched(cfg, q, k, v, out, b, 1, seq_k, O.BF16)
+    torch.cuda.synchronize()
+    got = to_host(out, np.uint16).reshape(h, d)
+    qh, kh, vh = to_host(q, np.uint16), to_host(k, np.uint16), to_host(v, np.uint16)
+    O.set_threads(8)
+    heads = (0, 1, 777, 2039)
+    for hd in heads:
+        ref = O.mha_rows(qh, kh, vh, h, d, (hd, hd + 1), (0, 1), kv_heads=kvh, dtype=O.BF16)
+        assert_close(O.to_f32(got[hd], O.BF16), O.to_f32(ref.reshape(h, d)[hd], O.BF16), TOL[O.BF16],
+                     elem_tol=None, what=f"head {hd}")

@@ -60,11 +60,21 @@ def test_multi_axis_rope(backend, dt, b, s, h, base, latent, side, dims):
     assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], what="multi-axis")
 
 
-GATES = ["SwiGLU", "GeGLU", "GeGLUTanh", "SiGLU", "GLU", "ReGLU", "LinGLU"]
+GATES = ["SwiGLU", "GeGLU", "GeGLUTanh", "SiGLU", "GLU", "ReGLU", "LinGLU", "SeGLU"]
+
+
+# kinds whose arithmetic the kernel evaluates operation by operation as the oracle
+# does (FastExp32, IEEE division and products), so every dtype is bit-exact
+BIT_EXACT_KINDS = (0, 3, 4, 5, 6, 7)
+
+
+def _same(got, ref, dt):
+    return np.array_equal(got.view(np.uint32) if dt == O.F32 else got,
+                          ref.view(np.uint32) if dt == O.F32 else ref)
 
 
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16])
-@pytest.mark.parametrize("kind", range(7))
+@pytest.mark.parametrize("kind", range(len(GATES)))
 @pytest.mark.parametrize("count", [1, 13, 4096, 14336 * 3 + 5])
 def test_gated_tensors(backend, dt, kind, count):
     g = encode(seeded(40 + count + kind, (count,), 0.0, 3.0), dt)
@@ -73,23 +83,27 @@ def test_gated_tensors(backend, dt, kind, count):
     out = empty_dev((count,), NP[dt])
     getattr(backend, GATES[kind] + "Tensors")(out, to_dev(g), to_dev(u), count, dt)
     got = to_host(out, NP[dt])
-    if kind in (0, 3, 4, 5, 6):
-        # FastExp32 / IEEE division evaluated op by op: identical to the oracle
-        assert np.array_equal(got.view(np.uint32) if dt == O.F32 else got,
-                              ref.view(np.uint32) if dt == O.F32 else ref), GATES[kind]
+    if kind in BIT_EXACT_KINDS:
+        assert _same(got, ref, dt), GATES[kind]
     else:
         assert_close(decode(got, dt), decode(ref, dt), TOL[dt], what=GATES[kind])
 
 
-@pytest.mark.parametrize("dt", [O.F32, O.BF16])
-@pytest.mark.parametrize("kind", [0, 1])
-def test_gated_packed(backend, dt, kind):
-    batch, half = 6, 1024
-    p = encode(seeded(50 + kind, (batch, 2 * half)), dt)
-    ref = decode(O.gated_packed(kind, p, dt), dt)
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16])
+@pytest.mark.parametrize("kind", range(len(GATES)))
+@pytest.mark.parametrize("batch,half", [(6, 1024), (3, 37)])
+def test_gated_packed(backend, dt, kind, batch, half):
+    """Packed rows [gate | up] (half 1024: the 16-byte vector path; half 37: the
+    element path, rows not vector-aligned)."""
+    p = encode(seeded(50 + kind + half, (batch, 2 * half), 0.0, 2.0), dt)
+    ref = O.gated_packed(kind, p, dt)
     out = empty_dev((batch, half), NP[dt])
     getattr(backend, GATES[kind])(out, to_dev(p), batch, half, dt)
-    assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], what="packed")
+    got = to_host(out, NP[dt])
+    if kind in BIT_EXACT_KINDS:
+        assert _same(got, ref, dt), GATES[kind]
+    else:
+        assert_close(decode(got, dt), decode(ref, dt), TOL[dt], what="packed " + GATES[kind])
 
 
 def test_fast_exp_edges_through_swiglu(backend):

@@ -34,7 +34,8 @@ def test_registry_semantics_match_the_reference():
 def test_hip_registrations():
     r = R.register_hip_kernels(R.Registry(), puter_amd.Backend())
     names = {k.Name for k in r.Snapshot()}
-    assert {"page_write", "page_gather", "layernorm", "swiglu", "geglu", "silu", "gelu", "cast",
+    assert {"page_write", "page_gather", "layernorm", "swiglu", "geglu", "geglu_tanh", "siglu", "glu",
+            "reglu", "linglu", "seglu", "silu", "gelu", "cast",
             "matmul", "multi_head_attention", "grouped_query_attention", "sliding_window_attention",
             "attention", "flash_attention", "int8_dequant", "int4_dequant", "int8_quant"} <= names
     assert all(k.Locations == [R.LOCATION_DEVICE] for k in r.Snapshot())
