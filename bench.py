@@ -378,6 +378,78 @@ def decode(torch, be, puter, fp8, return_fn=False):
     return res
 
 
+def pages(torch, be, puter, return_fns=False):
+    """The paged-KV hooks (execution/page_intrinsic.go:135-352) at configs[4]'s
+    pool (B64, ctx ~ U[512, 8192], page 16, 8 kv heads x 128 bf16: 2 KiB rows,
+    pages randomly permuted): KVPageWrite of one decode step (a row per
+    sequence at its next slot), of 4096 and of 16384 prefill rows (consecutive
+    tokens through a sequence's page table), and KVPageGather of every
+    sequence's pages in one call.  Algorithmic bytes: rows x 2 KiB read + the
+    same written, plus 8 B of (id, slot) per written row or 4 B of table per
+    gathered page.  A plain device copy of the prefill write's bytes is timed
+    beside it for context."""
+    import numpy as np
+    rng = np.random.default_rng(0x5EED0004)
+    B, KV, D, PS = 64, 8, 128, 16
+    inner, row_bytes = KV * D, KV * D * 2
+    ctx = rng.integers(512, 8193, B).astype(np.int32)
+    npages = (ctx + PS - 1) // PS
+    total = int(npages.sum()) + 1024          # room for 16384 fresh rows
+    perm = rng.permutation(total).astype(np.int32)
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0007)
+    pool = torch.randn(total * PS * inner, device="cuda", generator=gen).to(torch.bfloat16)
+    t = Timer(torch)
+    res, fns = {}, {}
+    # decode step: sequence i writes its token ctx_i at its page table's slot
+    first = np.concatenate([[0], np.cumsum(npages)[:-1]])
+    dec_ids = perm[first + (ctx - 1) // PS].astype(np.int32)
+    dec_offs = ((ctx - 1) % PS).astype(np.int32)
+    cases = [("decode_b64", dec_ids, dec_offs)]
+    for n in (4096, 16384):                   # a prefill's K rows into fresh pages
+        fresh = perm[total - 1024:total - 1024 + n // PS]
+        r = np.arange(n)
+        cases.append((f"prefill_{n}", fresh[r // PS].astype(np.int32), (r % PS).astype(np.int32)))
+    for name, ids, offs in cases:
+        n = ids.size
+        vals = torch.randn(n * inner, device="cuda", generator=gen).to(torch.bfloat16)
+        di, do = torch.from_numpy(ids).cuda(), torch.from_numpy(offs).cuda()
+        fn = (lambda v=vals, di=di, do=do, n=n:  # noqa: E731
+              be.KVPageWrite(pool, v, di, do, pool, total, PS, inner, n, 0, puter.BF16))
+        fns[f"page_write_{name}"] = fn
+        if return_fns:
+            continue
+        fn()
+        ms = t.graph(fn, 20) if n <= 4096 else t.time(fn, 20, warmup=3)
+        nbytes = n * (2 * row_bytes + 8)
+        res[f"page_write_{name}_us"] = round(ms * 1e3, 2)
+        res[f"page_write_{name}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        res[f"page_write_{name}_hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        if n == 16384:
+            src = vals
+            dst = torch.empty_like(src)
+            ms = t.time(lambda: dst.copy_(src), 20, warmup=3)
+            res["context_copy_prefill_16384_GBs"] = round(n * 2 * row_bytes / (ms * 1e-3) / 1e9, 1)
+            del dst
+    # gather: every sequence's pages back to back in one table
+    table = torch.from_numpy(perm[:int(npages.sum())].copy()).cuda()
+    out_rows = int(npages.sum()) * PS
+    out = torch.empty(out_rows * inner, device="cuda", dtype=torch.bfloat16)
+    fn = lambda: be.KVPageGather(pool, table, out, total, PS, inner, out_rows, 0, puter.BF16)  # noqa: E731
+    fns["page_gather_b64"] = fn
+    if return_fns:
+        return fns
+    fn()
+    ms = t.time(fn, 20, warmup=3)
+    nbytes = out_rows * 2 * row_bytes + table.numel() * 4
+    res["page_gather_b64_us"] = round(ms * 1e3, 1)
+    res["page_gather_b64_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    res["page_gather_b64_hbm_frac"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    be.CheckStatus()
+    del pool, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def matmul_bf16(torch, be, puter):
     """Matmul in bf16 (f32 accumulation) on the MFMA GEMM: a square 8192^3, the
     MLP up-projection shape rows 8192 x inner 4096 x cols 14336, and decode-step
@@ -677,8 +749,9 @@ def profile_workload(torch, be, puter, spec, launches):
     bf16 on one shape, each launch on the next window of 1 GiB pools so none is
     served from the 256 MB last-level cache, then one 1 GiB calibration copy),
     `stream` (the 2-read/2-write stream probe in its three launch shapes),
-    `prefill` (configs[3]), `decode_bf16` / `decode_fp8` (configs[4]).  Each
-    launch is preceded by nothing else on the stream."""
+    `prefill` (configs[3]), `decode_bf16` / `decode_fp8` (configs[4]), `pages`
+    (the page write / gather legs at configs[4]'s pool).  Each launch is preceded
+    by nothing else on the stream."""
     if spec.startswith("norm:"):
         r, h = (int(x) for x in spec[5:].split("x"))
         gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
@@ -714,6 +787,10 @@ def profile_workload(torch, be, puter, spec, launches):
         fn = decode(torch, be, puter, spec == "decode_fp8", return_fn=True)
         for _ in range(launches):
             fn()
+    elif spec == "pages":
+        for name, fn in pages(torch, be, puter, return_fns=True).items():
+            for _ in range(launches):
+                fn()
     else:
         raise SystemExit(f"unknown workload {spec}")
     torch.cuda.synchronize()
@@ -769,11 +846,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="norm,rope,prefill,decode,matmul,block,cpu,traffic")
+    ap.add_argument("--only", default="norm,rope,prefill,decode,pages,matmul,block,cpu,traffic")
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run the dominant kernel N times plus a 1 GiB calibration copy")
     ap.add_argument("--profile-workload", default="", metavar="NAME",
-                    help="only run one counter-collection workload: norm:RxH, stream, prefill, decode_bf16, decode_fp8")
+                    help="only run one counter-collection workload: norm:RxH, stream, prefill, decode_bf16, "
+                         "decode_fp8, pages")
     ap.add_argument("--profile-launches", type=int, default=5, metavar="N")
     ap.add_argument("--profile-matmul", type=int, default=0, metavar="N",
                     help="only run the bf16 Matmul 8192^3 N times (counter collection)")
@@ -818,6 +896,10 @@ def main():
         configs.update(decode(torch, be, puter, False))
         configs.update(decode(torch, be, puter, True))
         log("decode done")
+    if "pages" in only:
+        configs.update(pages(torch, be, puter))
+        log(f"pages: write 16384 rows {configs['page_write_prefill_16384_GBs']} GB/s, "
+            f"gather {configs['page_gather_b64_GBs']} GB/s")
     if "matmul" in only:
         configs.update(matmul_bf16(torch, be, puter))
         log(f"matmul bf16: {configs['matmul_bf16_8192c_TFLOPs']} TFLOP/s at 8192^3")

@@ -225,6 +225,54 @@ def test_page_write_fp8_duplicate_slots_last_row_wins(backend):
     backend.CheckStatus()
 
 
+@pytest.mark.parametrize("dt,inner,rows", [(O.BF16, 1024, 20000), (O.F32, 6, 70001), (O.F8E4M3, 1024, 16384)])
+def test_page_write_prefill_sized_duplicates_far_apart(backend, dt, inner, rows):
+    """A prefill-sized KVPageWrite (16K to 70K rows: 16 to 128 rows per block,
+    2 KiB rows on the 16-byte path, 24-byte rows on the 4-byte path with a unit
+    count that is not a power of two, and the fp8 quantising write) whose
+    repeated (page, slot) pairs sit far apart: a tenth of the rows reuse the slot
+    of a random earlier row, the first and last rows share a slot, two adjacent
+    rows share one, and one slot is hit in three distant blocks.  The reference
+    copies the rows in order, so the last row of each slot wins
+    (device/cpu/shape/page_generic.go:23-27); the pool must equal the oracle's
+    bit for bit."""
+    backend.CheckStatus()
+    rng = np.random.default_rng(rows + inner + dt)
+    ps = 16
+    pages = rows // ps + 8
+    slot = rng.permutation(pages * ps)[:rows].astype(np.int64)
+    reuse = rng.choice(np.arange(1000, rows), rows // 10, replace=False)
+    for r in np.sort(reuse):
+        slot[r] = slot[rng.integers(0, r)]
+    slot[rows - 1] = slot[0]
+    slot[101] = slot[100]
+    slot[rows // 3] = slot[rows // 2] = slot[7]
+    ids, offs = (slot // ps).astype(np.int32), (slot % ps).astype(np.int32)
+    assert np.unique(slot).size < rows - rows // 20
+    if dt == O.F8E4M3:
+        kvh, hd = 8, 128
+        scales = (rng.random(kvh).astype(np.float32) + 0.5) / 64
+        vals = encode(rng.normal(0, 1, (rows, inner)).astype(np.float32), O.BF16)
+        storage = rng.integers(0, 256, pages * ps * inner).astype(np.uint8)
+        ref = O.page_write_fp8(storage, vals, ids, offs, ps, kvh, hd, scales, O.BF16)
+        d = to_dev(storage)
+        backend.KVPageWriteFP8(d, to_dev(vals), to_dev(ids), to_dev(offs), pages, ps, kvh, hd, rows, 0,
+                               to_dev(scales), O.BF16)
+        assert np.array_equal(to_host(d, np.uint8), ref)
+    else:
+        es = np.dtype(NP[dt]).itemsize
+        bits = np.uint32 if es == 4 else np.uint16
+        storage = rng.integers(0, 1 << (8 * es), pages * ps * inner, dtype=np.uint64).astype(bits)
+        vals = rng.integers(0, 1 << (8 * es), rows * inner, dtype=np.uint64).astype(bits)
+        if es == 4:
+            storage, vals = storage.view(np.float32), vals.view(np.float32)
+        ref = O.page_write(storage, vals, ids, offs, ps, inner)
+        d = to_dev(storage)
+        backend.KVPageWrite(d, to_dev(vals), to_dev(ids), to_dev(offs), d, pages, ps, inner, rows, 0, dt)
+        assert np.array_equal(to_host(d, storage.dtype).view(np.uint8), ref.view(np.uint8))
+    backend.CheckStatus()
+
+
 # -------------------------------------------------------------- attention --
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16])
 @pytest.mark.parametrize("sq,sk,h,kvh,d,causal", [
