@@ -649,12 +649,15 @@ def test_paged_decode_pool_beyond_4gib(backend, kv_dt):
     assert_close(O.to_f32(out, od), O.to_f32(ref, od), TOL[O.BF16], elem_tol=None, what="paged decode > 4 GiB")
 
 
-def test_paged_decode_fp8_value_codes_exact(backend):
+@pytest.mark.parametrize("kvh", [1, 2])
+def test_paged_decode_fp8_value_codes_exact(backend, kvh):
     """One live token per sequence: its softmax weight is exactly 1, so the output
     is the token's V row widened from fp8 and narrowed to bf16, bit for bit.  Two
     sequences hold all 256 E4M3 codes in their V rows (NaN codes give NaN), which
-    pins the kernel's fp8 -> bf16 widening code by code (convert/fp8_f32.go)."""
-    h = kvh = 1
+    pins the kernel's fp8 -> bf16 widening code by code (convert/fp8_f32.go).
+    With two kv heads (the kernel that takes a pair of heads per block) head 1
+    holds the codes in reverse order, so a head or dim placed wrongly fails."""
+    h = kvh
     d, ps = 128, 16
     ctx = np.array([1, 1], np.int32)
     table = np.array([[0], [1]], np.int32)
@@ -662,15 +665,19 @@ def test_paged_decode_fp8_value_codes_exact(backend):
     kp = np.zeros((2, ps, kvh, d), np.uint8)
     vp = np.zeros((2, ps, kvh, d), np.uint8)
     codes = np.arange(256, dtype=np.uint8)
-    vp[0, 0, 0] = codes[:128]
-    vp[1, 0, 0] = codes[128:]
+    per_head = [codes, codes[::-1]]
+    for hh in range(kvh):
+        vp[0, 0, hh] = per_head[hh][:128]
+        vp[1, 0, hh] = per_head[hh][128:]
     ks = vs = np.ones(kvh, np.float32)
     out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, 2, h, kvh, d, O.F8E4M3, ks, vs)
-    got = O.to_f32(out.reshape(-1), O.BF16)
-    want = O.to_f32(codes, O.F8E4M3)
-    nan = np.isnan(want)
-    assert np.array_equal(np.isnan(got), nan)
-    assert np.array_equal(got[~nan], want[~nan])   # -0 sums to +0, as the reference's 0 + 1 * v does
+    got = O.to_f32(out.reshape(2, h, d), O.BF16)
+    for hh in range(kvh):
+        want = O.to_f32(per_head[hh], O.F8E4M3).reshape(2, d)
+        g = got[:, hh]
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(g), nan), hh
+        assert np.array_equal(g[~nan], want[~nan]), hh   # -0 sums to +0, as the reference's 0 + 1 * v does
 
 
 # group sizes 1, 2, 4, 8 (compiled in) and 3, 5, 7, 16 (read at run time); kv head
