@@ -96,8 +96,10 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     using P8 = typename std::conditional<H16, f16x8_t, bf16x8_t>::type;   // MFMA operand
     using PE = typename std::conditional<H16, _Float16, __bf16>::type;
     // per-wave 32-row tiles: K rows (256 bytes 16-bit, 128 fp8), then V rows (fp8
-    // widened to bf16: 256 bytes), then the o merge
-    __shared__ __attribute__((aligned(1024))) char k_lds[4][32 * 256];
+    // widened to bf16: 256 bytes), then the o merge (rows of kORow floats: the
+    // 4 extra floats put the heads' rows on different banks)
+    constexpr int kORow = D + 4;
+    __shared__ __attribute__((aligned(1024))) char k_lds[4][32 * 256 + 256];
     __shared__ float ml_lds[4][GT ? GT : 16][2];
 
     // Block order.  Consecutive dispatch ids go round-robin over the 8 XCDs; XCD x
@@ -174,13 +176,18 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                 vb[k] = ld_stream(reinterpret_cast<const uint4 *>(vpool + off));
             }
         }
-        // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero
+        // B operand (Q^T): lane holds Q[head l16][32t + 8grp .. +7]; heads >= G are zero.
+        // fp8 rows take the dims in another order, the same for K and Q (the dot is
+        // a sum over all dims): MFMAs 2p and 2p + 1 give lane group grp dims
+        // 64p + 16grp .. + 7 and + 8 .. + 15, 16 consecutive codes of a K row, read
+        // as one 16-byte piece
         P8 qb[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             uint4 u = make_uint4(0, 0, 0, 0);
+            const int dim0 = W16 ? 32 * t + 8 * grp : 64 * (t >> 1) + 16 * grp + 8 * (t & 1);
             if (l16 < G)
-                u = *reinterpret_cast<const uint4 *>(a.q + ((int64_t)b * a.heads + (int64_t)kvh * G + l16) * D + 32 * t + 8 * grp);
+                u = *reinterpret_cast<const uint4 *>(a.q + ((int64_t)b * a.heads + (int64_t)kvh * G + l16) * D + dim0);
             qb[t] = __builtin_bit_cast(P8, u);
         }
         const uint64_t live = __ballot(myrow >= 0);   // token t live iff bit t
@@ -191,9 +198,9 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
         // scores S^T[token, head], 32 tokens at a time: K rows -> the wave's LDS
         // tile, then A = tile rows 16i + l16, B = Q^T; lane: head l16, tokens
         // 16i + 4grp + r.  bf16 rows keep 16-byte piece c at c ^ (r % 16); fp8 rows
-        // (128 bytes) keep it at c ^ ((r / 2) % 8), i.e. 8-byte unit u at
-        // u ^ 2 ((r / 2) % 8): the 16 rows an operand read touches then fall on
-        // distinct banks (rows r and r ^ 1 lie 128 bytes apart)
+        // (128 bytes, one 128-byte bank line each) keep it at c ^ (r % 8), so the
+        // 8 rows of the 8 lanes an LDS cycle serves for a 16-byte read or write
+        // fall on distinct banks
         f32x4_t s[4];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -208,7 +215,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int r = 8 * k + g8;
-                    *reinterpret_cast<uint4 *>(tile + r * 128 + ((l8 ^ ((r >> 1) & 7)) << 4)) = kb[4 * half + k];
+                    *reinterpret_cast<uint4 *>(tile + r * 128 + ((l8 ^ (r & 7)) << 4)) = kb[4 * half + k];
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -216,11 +223,18 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
             for (int i = 0; i < 2; ++i) {
                 f32x4_t acc_s = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
                 const int row = 16 * i + l16;
+                uint4 k8[2];   // fp8: 16-byte pieces 4p + grp of the row (codes for MFMAs 2p, 2p + 1)
+                if constexpr (!W16) {
+#pragma unroll
+                    for (int pp = 0; pp < 2; ++pp)
+                        k8[pp] = *reinterpret_cast<const uint4 *>(tile + row * 128 + (((4 * pp + grp) ^ (row & 7)) << 4));
+                }
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     uint4 kv;
                     if constexpr (W16) kv = *reinterpret_cast<const uint4 *>(tile + row * 256 + (((4 * t + grp) ^ l16) << 4));
-                    else kv = fp8x8_to_bf16(*reinterpret_cast<const uint2 *>(tile + row * 128 + (((4 * t + grp) ^ (2 * ((l16 >> 1) & 7))) << 3)));
+                    else kv = (t & 1) ? fp8x8_to_bf16(make_uint2(k8[t >> 1].z, k8[t >> 1].w))
+                                      : fp8x8_to_bf16(make_uint2(k8[t >> 1].x, k8[t >> 1].y));
                     if constexpr (H16) acc_s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(P8, kv), qb[t], acc_s, 0, 0, 0);
                     else acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(P8, kv), qb[t], acc_s, 0, 0, 0);
                 }
@@ -312,6 +326,9 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                     *reinterpret_cast<uint4 *>(tile + r * 256 + ((l16 ^ vsw(r)) << 4)) = w;
                 }
             } else {   // 16 fp8 codes (dims 16 l8 .. + 15) -> two bf16 pieces 2 l8, 2 l8 + 1
+                // lanes l8 >= 4 write their odd piece first, so each of the two writes
+                // puts the 8 lanes of one LDS cycle (one row) on 8 distinct banks
+                const int odd = (l8 >> 2) & 1;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int kk = 4 * st + k, r = 8 * k + g8;
@@ -320,10 +337,10 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
                         const uint32_t keep = ((live >> (8 * kk + g8)) & 1) ? 0xFFFFFFFFu : 0u;
                         raw = make_uint4(raw.x & keep, raw.y & keep, raw.z & keep, raw.w & keep);
                     }
-                    const uint4 w0 = fp8x8_to_bf16(make_uint2(raw.x, raw.y));
-                    const uint4 w1 = fp8x8_to_bf16(make_uint2(raw.z, raw.w));
-                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8) ^ vsw(r)) << 4)) = w0;
-                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8 + 1) ^ vsw(r)) << 4)) = w1;
+                    const uint2 first = odd ? make_uint2(raw.z, raw.w) : make_uint2(raw.x, raw.y);
+                    const uint2 second = odd ? make_uint2(raw.x, raw.y) : make_uint2(raw.z, raw.w);
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8 + odd) ^ vsw(r)) << 4)) = fp8x8_to_bf16(first);
+                    *reinterpret_cast<uint4 *>(tile + r * 256 + (((2 * l8 + 1 - odd) ^ vsw(r)) << 4)) = fp8x8_to_bf16(second);
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -352,7 +369,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     // merge the four waves: (m, l) per head and o[head][128] through LDS (the o
     // rows reuse the tiles, so every wave must be done with its tile first)
     __syncthreads();
-    float *o_lds = reinterpret_cast<float *>(&k_lds[0][0]);   // [4][G][128]
+    float *o_lds = reinterpret_cast<float *>(&k_lds[0][0]);   // [4][G][kORow]
     if (grp == 0 && l16 < G) {
         ml_lds[wave][l16][0] = m_w;
         ml_lds[wave][l16][1] = l_w;
@@ -360,7 +377,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     if (l16 < G) {
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt)
-            *reinterpret_cast<float4 *>(o_lds + (wave * G + l16) * D + 16 * mt + 4 * grp) =
+            *reinterpret_cast<float4 *>(o_lds + (wave * G + l16) * kORow + 16 * mt + 4 * grp) =
                 make_float4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]);
     }
     __syncthreads();
@@ -376,7 +393,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
             const float mw = ml_lds[w][h][0];
             const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
             L += ml_lds[w][h][1] * f;
-            O += o_lds[(w * G + h) * D + d] * f;
+            O += o_lds[(w * G + h) * kORow + d] * f;
         }
         const int64_t slot = slot0 + (int64_t)h * a.max_splits;
         a.part_o[slot * D + d] = O;
