@@ -198,6 +198,23 @@ def norm_legs(torch, be, puter):
             assert rc == 0, rc
         t = timer.time(probe, 20, warmup=3)
         res[f"stream_2r2w_{name}_GBs"] = round(4 * 16 * vectors / (t * 1e-3) / 1e9, 1)
+    # the same 2-read/2-write stream at the sweep's 1024-row sizes (the ceiling of its
+    # smallest shapes), timed as the sweep times them: 20 launches, each on the next
+    # window of the 1 GiB buffers, captured in a HIP graph and replayed
+    for hh in HIDDEN:
+        vec = 1024 * hh * 2 // 16
+        nwin = 2 * n // (16 * vec)
+        for shape, name in ((0, "flat"), (2, "wave_row")):
+            win = [0]
+
+            def probe_small(shape=shape, vec=vec, nwin=nwin, win=win):
+                off = (win[0] % nwin) * vec * 16
+                win[0] += 1
+                rc = be.lib.puter_hip_stream_probe(*(C.c_void_p(t.data_ptr() + off) for t in (x, br, y, d)), vec,
+                                                   shape, C.c_void_p(st()))
+                assert rc == 0, rc
+            t = timer.graph(probe_small, 20)
+            res[f"stream_2r2w_1024x{hh}_{name}_GBs"] = round(4 * 16 * vec / (t * 1e-3) / 1e9, 1)
     del x, br, y, d
     torch.cuda.empty_cache()
     return res
