@@ -98,9 +98,13 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     // per-wave 32-row tiles: K rows (256 bytes 16-bit, 128 fp8), then V rows (fp8
     // widened to bf16: 256 bytes), then the o merge (rows of kORow floats: the
     // 4 extra floats put the heads' rows on different banks)
+    // With a compiled group size (at most 8 heads) the padded o rows and the
+    // (m, l) pairs fit in the 32 KB of tiles, so a block takes exactly 32 KB and
+    // five fit on a CU; the run-time group size (up to 16 heads) takes 33 KB.
     constexpr int kORow = D + 4;
-    __shared__ __attribute__((aligned(1024))) char k_lds[4][32 * 256 + 256];
-    __shared__ float ml_lds[4][GT ? GT : 16][2];
+    constexpr int kTile = GT ? 32 * 256 : 32 * 256 + 256;
+    __shared__ __attribute__((aligned(1024))) char k_lds[4][kTile];
+    __shared__ float ml_spill[GT ? 1 : 4 * 16 * 2];
 
     // Block order.  Consecutive dispatch ids go round-robin over the 8 XCDs; XCD x
     // runs a group of gk kv heads of chunk (split, sequence) 8n + x one after
@@ -370,6 +374,9 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     // rows reuse the tiles, so every wave must be done with its tile first)
     __syncthreads();
     float *o_lds = reinterpret_cast<float *>(&k_lds[0][0]);   // [4][G][kORow]
+    // [4][G][2]: after the o rows inside the tiles, or beside them (run-time G)
+    float(*ml_lds)[GT ? GT : 16][2] = reinterpret_cast<float(*)[GT ? GT : 16][2]>(
+        GT ? o_lds + 4 * (GT ? GT : 16) * kORow : ml_spill);
     if (grp == 0 && l16 < G) {
         ml_lds[wave][l16][0] = m_w;
         ml_lds[wave][l16][1] = l_w;
