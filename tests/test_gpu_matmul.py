@@ -50,6 +50,33 @@ def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
 
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("rows,inner,cols", [(4000, 264, 4104), (1000, 520, 1032), (513, 64, 2056)])
+def test_matmul_16bit_exact_integer_products(backend, dt, rows, inner, cols):
+    """Every output element, bit for bit: operands are small integers (|a| <= 3,
+    |b| <= 2), so each partial sum is an integer below 2^24 and exact in f32 in any
+    summation order; the result must be the f32 sum of compute.go:74-92 rounded
+    once to the 16-bit format, i.e. the oracle's narrowing of numpy's exact integer
+    product.  The first shape takes the 8-wave 256 x 256 kernel, the others the
+    4-wave 256 x 128 one; all have ragged row and column tiles (the epilogue's
+    bounds) and K tails.  A misplaced, missing or duplicated element fails here,
+    where a normwise bar could hide it."""
+    rng = np.random.default_rng(rows + 7 * inner + 3 * cols)
+    ai = rng.integers(-3, 4, (rows, inner))
+    bi = rng.integers(-2, 3, (inner, cols))
+    a = O.from_f32(ai.astype(np.float32), dt)
+    b = O.from_f32(bi.astype(np.float32), dt)
+    assert np.array_equal(O.to_f32(a, dt), ai) and np.array_equal(O.to_f32(b, dt), bi)
+    exact = (ai @ bi).astype(np.float32)   # |sum| <= 6 * inner < 2^24: exact
+    out = empty_dev((rows, cols), np.uint16)
+    out.fill_(0x7FC0)   # a NaN pattern in both formats' sign/exponent field: unwritten cells show
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, dt)
+    got = to_host(out, np.uint16)
+    want = O.from_f32(exact, dt)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{bad.shape[0]} cells differ, e.g. {bad[:4].tolist()}: {got[tuple(bad[:4].T)]} vs {want[tuple(bad[:4].T)]}"
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("rows,inner,cols", [(64, 4096, 4096), (1, 4104, 2056), (200, 1000, 1024),
                                              (256, 512, 14336), (3, 64, 8), (500, 1032, 4104), (256, 512, 1024)])
 def test_matmul_16bit_skinny_split_k(backend, dt, rows, inner, cols):
