@@ -3,16 +3,17 @@
 // (dispatchMatmul: F32, F64, F16, BF16; the 16-bit formats widen to f32, sum in
 // f32 and store the sum rounded to nearest even, compute.go:74-92).
 //
-// bf16 / f16: MFMA GEMM, two tile shapes from one template (NW = waves along N):
-//   NW = 4 (large problems): a 512-thread block (8 waves, 2 x 4) computes a
-//     256 x 256 output tile, K advancing 64 at a time, one block per CU;
-//   NW = 2 (fewer than 160 such tiles): a 256-thread block (4 waves, 2 x 2)
-//     computes a 256 x 128 tile, K advancing 32, two blocks per CU.
-// Wave (wm, wn) owns rows 128 wm .. +127 and columns 64 wn .. +63 as 4 x 2
-// v_mfma_f32_32x32x16 accumulators.  The A (256 x BK) and B (BK x 64 NW)
-// slices are copied HBM -> LDS by buffer_load ... lds, double buffered (NW = 4)
-// or on a 3-stage ring (NW = 2), each slice's copies issued before the slice
-// ahead of it is computed.  The block computes
+// bf16 / f16: MFMA GEMM, two tile shapes from one template (NW = waves along N,
+// MT = 32-row accumulator blocks per wave), K advancing 64 at a time:
+//   NW = 4, MT = 4: a 512-thread block (8 waves, 2 x 4) computes a 256 x 256
+//     output tile, one block per CU;
+//   NW = 2, MT = 2: a 256-thread block (4 waves, 2 x 2) computes a 128 x 128
+//     tile, two blocks per CU; taken where its rounds of blocks over the CUs
+//     cost less (mfma_small_tiles).
+// Wave (wm, wn) owns rows 32 MT wm .. +32 MT - 1 and columns 64 wn .. +63 as MT x 2
+// v_mfma_f32_32x32x16 accumulators.  The A (64 MT x 64) and B (64 x 64 NW)
+// slices are copied HBM -> LDS by buffer_load ... lds, double buffered, each
+// slice's copies issued before the slice ahead of it is computed.  The block computes
 // C^T = B^T . A^T so that a lane's accumulator column is one output row and its
 // registers hold runs of 4 consecutive output columns (the epilogue regroups them
 // in LDS into whole 128-byte row pieces before storing):
@@ -23,8 +24,8 @@
 //     0..15 of rows k0..k0+3 transposed);
 //   B operand (A^T[k, m]): 8 consecutive k of row m of the A slice, one 16-byte
 //     LDS read.
-// LDS layouts: the A slice keeps rows of 2 BK bytes (8 / NW rows per 256 bytes)
-// with 16-byte chunk c of row r at c ^ ((r / (8 / NW)) % 2 NW); the B slice keeps
+// LDS layouts: the A slice keeps rows of 128 bytes (two per 256 bytes) with
+// 16-byte chunk c of row r at c ^ ((r / 2) % 8); the B slice keeps
 // rows of 128 NW bytes with chunk c of row r at c ^ 4 (r % 4); both make the
 // operand reads bank-conflict free.  Buffer descriptors end with the matrices,
 // so rows past M (A) or K (B) arrive as zeros; in the last K slice, A chunks past
@@ -44,6 +45,7 @@
 // order (matmulFloat64Scalar, device/cpu/matmul/select_generic.go:39-...).
 #include "common.hpp"
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 #include <type_traits>
@@ -209,7 +211,6 @@ static unsigned generic_blocks(int64_t n) { return (unsigned)std::min<int64_t>((
 
 // ------------------------------------------------------------------ MFMA --
 namespace mm {
-constexpr int BM = 256;
 constexpr int BUF_WORD3 = 0x00020000; // raw buffer, dword access
 constexpr int OOB = 0x7FFFFFF0;       // an offset past every descriptor's range
 }  // namespace mm
@@ -240,14 +241,15 @@ __device__ __forceinline__ mm_f32x16 mm_mfma(const mm_i16x4 (&a)[2], const uint4
                                                       __builtin_bit_cast(mm_f16x8, b), acc, 0, 0, 0);
 }
 
-template <int DT, int NW, int BK, int S>
-__global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(MmArgs p) {
+template <int DT, int NW, int MT, int BK, int S>
+__global__ __launch_bounds__(128 * NW, NW == 4 ? 1 : 2) void matmul_mfma_kernel(MmArgs p) {
     using namespace mm;
-    constexpr int BN = 64 * NW;
+    constexpr int BM = 64 * MT, BN = 64 * NW;   // 2 waves along M of 32 MT rows, NW along N of 64 columns
+    constexpr int WR = 32 * MT;                 // rows per wave
     constexpr int RA = 2 * BK, RB = 2 * BN;            // LDS row bytes of the A and B slices
     constexpr int A_BYTES = BM * RA, B_BYTES = BK * RB;
     constexpr int AC = RA / 16;                         // 16-byte chunks per A row
-    constexpr int APW = RA / 4 / (2 * NW);              // A copies per wave per slice
+    constexpr int APW = BM * RA / 1024 / (2 * NW);      // A copies per wave per slice
     constexpr int BPW = BK / 16;                        // B copies per wave per slice
     constexpr int KS = BK / 16;                         // k-steps per slice
     // a ring of S slices in separate arrays, so the compiler can tell the slice being
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
     {
         const int sw = (l32 / (256 / RA)) % AC;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) ard[s] = (128 * wm + l32) * RA + (((2 * s + g) ^ sw) << 4);
+        for (int s = 0; s < KS; ++s) ard[s] = (WR * wm + l32) * RA + (((2 * s + g) ^ sw) << 4);
     }
     int brd[2];
     {
@@ -336,9 +338,9 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
                     bd, (mm_lds_void *)(bs + ((BK / (2 * NW)) * wave + (1024 / RB) * i) * RB), 16, boff[i], 0, 0, 0);
     };
 
-    mm_f32x16 acc[4][2];
+    mm_f32x16 acc[MT][2];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = (mm_f32x16){};
 
@@ -353,11 +355,11 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
                 bt[nt][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)bp);
                 bt[nt][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mm_lds_i16x4 *)(bp + 4 * RB));
             }
-            uint4 af[4];
+            uint4 af[MT];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) af[mt] = *reinterpret_cast<const uint4 *>(as + ard[s] + mt * 32 * RA);
+            for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const uint4 *>(as + ard[s] + mt * 32 * RA);
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mm_mfma<DT>(bt[nt], af[mt], acc[mt][nt]);
         }
@@ -399,31 +401,39 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
     for (int i = 0; i < S; ++i)
         if (kt + i < nk) slice(kt + i, i);
 
-    // Epilogue.  Lane holds C[m0 + 128 wm + 32 mt + l32][n0 + 64 wn + 32 nt + 8 (r/4) +
+    // Epilogue.  Lane holds C[m0 + WR wm + 32 mt + l32][n0 + 64 wn + 32 nt + 8 (r/4) +
     // 4 g + r%4]: stored straight from the accumulators, each store instruction would
-    // write 16 bytes into each of 32 rows.  Instead the wave parks its 128 x 64 block,
+    // write 16 bytes into each of 32 rows.  Instead the wave parks its WR x 64 block,
     // narrowed, in LDS (the slice buffers are free after the last slice's barrier) and
     // stores it back as 8 whole 128-byte row pieces per instruction, non-temporal (C is
     // not re-read by this kernel): +2 to +7% on 8192^3, 8192 x 4096 x 14336 and 4096^3.
-    // Wave w owns 8 KB halves 2w and 2w + 1 (rows 0..63 and 64..127 of its block, 128
-    // bytes a row); row r keeps its 16-byte chunk c (8 columns) at c ^ (r % 8), so the
-    // 8-byte writes (16 rows per LDS cycle) and the 16-byte reads (one row per cycle)
-    // are free of bank conflicts.
+    // The wave owns HW 8 KB halves of the ring (64 rows of 128 bytes each: halves
+    // HW w .. HW w + HW - 1, counted through the A buffers, then the B buffers); row r
+    // keeps its 16-byte chunk c (8 columns) at c ^ (r % 8), so the 8-byte writes (16
+    // rows per LDS cycle) and the 16-byte reads (one row per cycle) are free of bank
+    // conflicts.
     {
+        constexpr int HW = MT / 2, HA = A_BYTES / 8192, HB = B_BYTES / 8192;
+        static_assert(S * (HA + HB) >= 2 * NW * HW, "the ring holds every wave's block");
+        char *const bufs[8] = {as0, as1, as2, as3, bs0, bs1, bs2, bs3};
         auto half_region = [&](int j) __attribute__((always_inline)) -> char * {
-            if constexpr (NW == 4) {   // four 32 KB buffers
-                char *const base = j < 8 ? (j < 4 ? as0 : as1) : (j < 12 ? bs0 : bs1);
-                return base + (j & 3) * 8192;
-            } else {                   // three 16 KB A buffers, then 8 KB B buffers
-                static_assert(NW == 4 || (A_BYTES == 16384 && B_BYTES == 8192 && S == 3), "staging layout");
-                if (j < 6) return (j < 2 ? as0 : (j < 4 ? as1 : as2)) + (j & 1) * 8192;
-                return j == 6 ? bs0 : bs1;
-            }
-        };
-        char *const h0 = half_region(2 * wave), *const h1 = half_region(2 * wave + 1);
+            char *r = as0;
+            int base = 0;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            char *const hb = (mt < 2 ? h0 : h1) + (32 * (mt & 1) + l32) * 128;
+            for (int q = 0; q < 8; ++q) {
+                if ((q & 3) >= S) continue;
+                const int h = q < 4 ? HA : HB;
+                if (j >= base && j < base + h) r = bufs[q] + (j - base) * 8192;
+                base += h;
+            }
+            return r;
+        };
+        char *hs[HW];
+#pragma unroll
+        for (int hf = 0; hf < HW; ++hf) hs[hf] = half_region(HW * wave + hf);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            char *const hb = hs[mt >> 1] + (32 * (mt & 1) + l32) * 128;
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -441,35 +451,37 @@ __global__ __launch_bounds__(128 * NW, NW == 2 ? 2 : 1) void matmul_mfma_kernel(
         const int r8 = lane >> 3, c8 = lane & 7;
         const int col = n0 + 64 * wn + 8 * c8;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < WR / 8; ++i) {
             const int rr = 8 * (i & 7) + r8;   // row inside the half
-            const mm_u32x4 v = *reinterpret_cast<const mm_u32x4 *>((i < 8 ? h0 : h1) + rr * 128 + ((c8 ^ (rr & 7)) << 4));
-            const int row = m0 + 128 * wm + 8 * i + r8;
+            const mm_u32x4 v = *reinterpret_cast<const mm_u32x4 *>(hs[i >> 3] + rr * 128 + ((c8 ^ (rr & 7)) << 4));
+            const int row = m0 + WR * wm + 8 * i + r8;
             if (row < M && col < N)   // N % 8 == 0: a chunk is wholly inside or outside
                 __builtin_nontemporal_store(v, reinterpret_cast<mm_u32x4 *>(p.c + (int64_t)row * N + col));
         }
     }
 }
 
-// Launches the NW-wide MFMA kernel (NW = 4: 64-deep slices, 2 stages; NW = 2:
-// 32-deep slices on a 3-stage ring); returns 1 when the shape does not fit it.
-template <int DT, int NW>
+// Launches the MFMA kernel with NW waves along N and MT accumulator blocks of 32
+// rows per wave (256 x 256 tiles: NW = 4, MT = 4; 128 x 128: NW = 2, MT = 2), 64-deep
+// slices double buffered; returns 1 when the shape does not fit it.
+template <int DT, int NW, int MT>
 static int launch_mfma(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
                        hipStream_t s) {
-    constexpr int BK = NW == 4 ? 64 : 32, S = NW == 4 ? 2 : 3;
+    constexpr int BK = 64, S = 2;
+    constexpr int BM = 64 * MT;
     if (256 * K * 2 >= mm::OOB || BK * N * 2 >= mm::OOB || M > 0x3FFFFFFF || N > 0x3FFFFFFF) return 1;
     MmArgs p;
     p.a = static_cast<const uint16_t *>(left);
     p.b = static_cast<const uint16_t *>(right);
     p.c = static_cast<uint16_t *>(out);
     p.M = (int)M; p.N = (int)N; p.K = (int)K;
-    p.tiles_m = (int)((M + mm::BM - 1) / mm::BM);
+    p.tiles_m = (int)((M + BM - 1) / BM);
     p.tiles_n = (int)((N + 64 * NW - 1) / (64 * NW));
     p.groups_m = (p.tiles_m + 3) / 4;
     const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
     const int64_t blocks = (groups + 7) / 8 * 8 * 32;
     if (blocks > 0x7FFFFFFF) return 1;
-    matmul_mfma_kernel<DT, NW, BK, S><<<(unsigned)blocks, 128 * NW, 0, s>>>(p);
+    matmul_mfma_kernel<DT, NW, MT, BK, S><<<(unsigned)blocks, 128 * NW, 0, s>>>(p);
     return 0;
 }
 
@@ -903,6 +915,32 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
     return rc ? rc : fin;
 }
 
+// Compute units of the current device, cached per device (256 on MI355X).
+static int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Tile shape of the MFMA GEMM by wave quantisation: 256 x 256 tiles run one block
+// per CU, 128 x 128 tiles two; a full round of the small tiles does half the work
+// of a round of the large ones in 0.59 of its time (measured 1100 against 1300
+// TFLOP/s on large shapes), so the shape with the smaller rounds x cost wins.  Small
+// tiles: 2048^3 351 -> 623 TFLOP/s, 1024 x 4096 x 4096 385 -> 697, 6144 x 4096 x 4096
+// 956 -> 1081 (1.5 rounds of large tiles); large: 4096^3 1257 against 1070.
+static bool mfma_small_tiles(int64_t M, int64_t N) {
+    const int64_t cus = device_cus();
+    const int64_t large = ((M + 255) / 256) * ((N + 255) / 256), small = ((M + 127) / 128) * ((N + 127) / 128);
+    const int64_t r_large = (large + cus - 1) / cus, r_small = (small + 2 * cus - 1) / (2 * cus);
+    return 59 * r_small < 100 * r_large;
+}
+
 template <int DT>
 static int launch_matmul16(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
                            hipStream_t s, PartialsTarget tgt) {
@@ -933,12 +971,8 @@ static int launch_matmul16(void *out, const void *left, const void *right, int64
             const int rc = launch_skinny<DT>(out, left, right, M, K, N, s, tgt);
             if (rc != 1) return rc;
         }
-        // 256 x 256 tiles (one 8-wave block per CU) from 160 such tiles up; below that
-        // 256 x 128 tiles spread over more CUs win (measured: 128 tiles -14% wide,
-        // 168 and more +13-17%)
-        const int64_t wide_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-        const int rc = wide_tiles >= 160 ? launch_mfma<DT, 4>(out, left, right, M, K, N, s)
-                                         : launch_mfma<DT, 2>(out, left, right, M, K, N, s);
+        const int rc = mfma_small_tiles(M, N) ? launch_mfma<DT, 2, 2>(out, left, right, M, K, N, s)
+                                              : launch_mfma<DT, 4, 4>(out, left, right, M, K, N, s);
         if (rc == 0) return check_launch("matmul mfma");
     }
     matmul_generic_kernel<DT><<<generic_blocks(M * N), 256, 0, s>>>(out, left, right, M, K, N);

@@ -29,10 +29,12 @@ def test_matmul_16bit(backend, dt, rows, inner, cols):
 
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
-@pytest.mark.parametrize("rows,inner,cols", [(4000, 200, 4104), (4096, 1024, 4096)])
+@pytest.mark.parametrize("rows,inner,cols", [(4000, 200, 4000), (4096, 1024, 4096), (4000, 200, 4104)])
 def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
-    """Shapes with at least 256 output tiles of 256 x 256 take the 8-wave kernel
-    (64-deep K slices): the first with ragged rows, columns and a K tail.  The
+    """Shapes of 256 output tiles of 256 x 256 (one round over the 256 CUs) take
+    the 8-wave kernel, the first with ragged rows, columns and a K tail; 4000 x
+    4104 (272 such tiles, two rounds, against three of 128 x 128 tiles) the 4-wave
+    128 x 128 kernel.  The
     oracle checks one row in every 256-row band (all columns, so every tile) and
     the last row; the whole product is checked against numpy's f64 product of
     the same 16-bit inputs."""
@@ -50,14 +52,14 @@ def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
 
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
-@pytest.mark.parametrize("rows,inner,cols", [(4000, 264, 4104), (1000, 520, 1032), (513, 64, 2056)])
+@pytest.mark.parametrize("rows,inner,cols", [(4000, 264, 4000), (4000, 264, 4104), (1000, 520, 1032), (513, 64, 2056)])
 def test_matmul_16bit_exact_integer_products(backend, dt, rows, inner, cols):
     """Every output element, bit for bit: operands are small integers (|a| <= 3,
     |b| <= 2), so each partial sum is an integer below 2^24 and exact in f32 in any
     summation order; the result must be the f32 sum of compute.go:74-92 rounded
     once to the 16-bit format, i.e. the oracle's narrowing of numpy's exact integer
     product.  The first shape takes the 8-wave 256 x 256 kernel, the others the
-    4-wave 256 x 128 one; all have ragged row and column tiles (the epilogue's
+    4-wave 128 x 128 one; all have ragged row and column tiles (the epilogue's
     bounds) and K tails.  A misplaced, missing or duplicated element fails here,
     where a normwise bar could hide it."""
     rng = np.random.default_rng(rows + 7 * inner + 3 * cols)
@@ -168,8 +170,9 @@ def test_matmul_skinny_k_tail_never_reads_the_next_row(backend):
 
 
 def test_matmul_k_tail_never_reads_the_next_row(backend):
-    """inner = 40: the last 32-wide K slice holds 8 valid columns; the chunks past
-    inner must arrive as zeros, not as the next row's first elements.  Row 1 of
+    """64 rows (the split-K kernel), inner = 40: the one 64-deep K slice holds 40
+    valid columns; the chunks past inner must arrive as zeros, not as the next
+    row's first elements.  Row 1 of
     `left` starts with NaN: only output row 1 may be NaN."""
     rows, inner, cols = 64, 40, 128
     a32 = seeded(901, (rows, inner))
@@ -187,10 +190,12 @@ def test_matmul_k_tail_never_reads_the_next_row(backend):
     assert_close(got[keep], ref[keep], TOL[O.BF16], elem_tol=None, what="k tail")
 
 
-def test_matmul_wide_k_tail_never_reads_the_next_row(backend):
-    """The same isolation on the 8-wave kernel: inner = 72 leaves 8 valid columns
-    in the last 64-wide slice; only output row 1 may be NaN."""
-    rows, inner, cols = 4096, 72, 4096
+@pytest.mark.parametrize("rows,inner,cols,sample", [(4096, 72, 4096, [0, 2, 255, 256, 2047, 4095]),
+                                                    (1000, 72, 1032, [0, 2, 127, 128, 999])])
+def test_matmul_wide_k_tail_never_reads_the_next_row(backend, rows, inner, cols, sample):
+    """The same isolation on the MFMA GEMM, 256 x 256 tiles (4096 x 4096) and
+    128 x 128 tiles (1000 x 1032, ragged): inner = 72 leaves 8 valid columns in the
+    last 64-wide slice; only output row 1 may be NaN."""
     a32 = seeded(903, (rows, inner))
     a32[1, 0] = np.nan
     a = O.from_f32(a32, O.BF16)
@@ -202,7 +207,6 @@ def test_matmul_wide_k_tail_never_reads_the_next_row(backend):
     keep = np.ones(rows, bool)
     keep[1] = False
     assert np.isfinite(got[keep]).all()
-    sample = [0, 2, 255, 256, 2047, 4095]
     ref = O.to_f32(O.matmul(np.ascontiguousarray(a[sample]), b, O.BF16), O.BF16)
     assert_close(got[sample], ref, TOL[O.BF16], elem_tol=None, what="wide k tail")
 
