@@ -556,9 +556,10 @@ __global__ __launch_bounds__(512) void matmul16_small_kernel(uint16_t *__restric
     }
 }
 
-// ---------------------------------------------------------- skinny (M <= 512) --
+// ------------------------------------ skinny (M <= 512) and small outputs --
 // Decode-time projections (a few rows against a large weight matrix) are bound by
-// streaming `right` once.  A 256-thread block computes a 64 x 128 tile over one
+// streaming `right` once; the kernel also serves outputs too small to fill the
+// CUs with 128 x 128 tiles (see launch_matmul16).  A 256-thread block computes a 64 x 128 tile over one
 // chunk of K (split K, at most one wave of 512 blocks when split), copying 64-deep slices HBM -> LDS on a
 // 3-stage ring (two slices in flight per block, two blocks per CU); wave w owns
 // columns 32 w .. +31 as 2 accumulators (rows 0..31, 32..63).  LDS layouts: A rows
@@ -869,9 +870,10 @@ struct PartialsTarget {
     float *fixed = nullptr;
 };
 
+// min_depth > 0: chunks of K at least min_depth deep (fewer chunks otherwise).
 template <int DT>
 static int launch_skinny(void *out, const void *left, const void *right, int64_t M, int64_t K, int64_t N,
-                         hipStream_t s, PartialsTarget tgt) {
+                         hipStream_t s, PartialsTarget tgt, int64_t min_depth) {
     if (64 * K * 2 >= mm::OOB || sk::BK * N * 2 >= mm::OOB || N > 0x3FFFFFFF) return 1;
     const int64_t tiles_n = (N + sk::BN - 1) / sk::BN, tiles_m = (M + sk::BM - 1) / sk::BM;
     if (tiles_n > 0x7FFFFFFF) return 1;
@@ -883,6 +885,7 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
     // 11.0 -> 10.1; 4 lost on 64x14336x4096, 41.4 against 29.0)
     int64_t chunks = std::min<int64_t>(std::max<int64_t>(512 / (tiles_m * tiles_n), 1), slices);
     chunks = std::min<int64_t>(chunks, 8);
+    if (min_depth > 0) chunks = std::max<int64_t>(1, std::min<int64_t>(chunks, K / min_depth));
     const int64_t per = (slices + chunks - 1) / chunks;  // slices per chunk
     chunks = (slices + per - 1) / per;
     SkArgs p{static_cast<const uint16_t *>(left), static_cast<const uint16_t *>(right), static_cast<uint16_t *>(out),
@@ -967,8 +970,16 @@ static int launch_matmul16(void *out, const void *left, const void *right, int64
             }
             return check_launch("matmul");
         }
-        if (M <= 512) {
-            const int rc = launch_skinny<DT>(out, left, right, M, K, N, s, tgt);
+        // Rows <= 512 (decode-step projections) take the split-K kernel; so do more rows
+        // when 128 x 128 tiles would not fill one round of two blocks per CU, its 64 x
+        // 128 tiles and K chunks (each at least 1024 deep) spreading the work further
+        // (same process: 1024 x 8192 x 1024 198 -> 470 TFLOP/s, 768 x 16384 x 1024 148 ->
+        // 543, 2048^3 612 -> 651 unsplit; 1024^3 split four ways fell 165 -> 105, hence
+        // the depth floor; from one full round up the MFMA kernels win: 4096 x 1024 x
+        // 2048 845 against 601)
+        const bool few_tiles = ((M + 127) / 128) * ((N + 127) / 128) < 2 * (int64_t)device_cus();
+        if (M <= 512 || few_tiles) {
+            const int rc = launch_skinny<DT>(out, left, right, M, K, N, s, tgt, M <= 512 ? 0 : 1024);
             if (rc != 1) return rc;
         }
         const int rc = mfma_small_tiles(M, N) ? launch_mfma<DT, 2, 2>(out, left, right, M, K, N, s)

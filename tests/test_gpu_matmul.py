@@ -52,15 +52,17 @@ def test_matmul_16bit_wide_tiles(backend, dt, rows, inner, cols):
 
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
-@pytest.mark.parametrize("rows,inner,cols", [(4000, 264, 4000), (4000, 264, 4104), (1000, 520, 1032), (513, 64, 2056)])
+@pytest.mark.parametrize("rows,inner,cols", [(4000, 264, 4000), (4000, 264, 4104), (1000, 520, 1032), (513, 64, 2056),
+                                             (1000, 2048, 520)])
 def test_matmul_16bit_exact_integer_products(backend, dt, rows, inner, cols):
     """Every output element, bit for bit: operands are small integers (|a| <= 3,
     |b| <= 2), so each partial sum is an integer below 2^24 and exact in f32 in any
     summation order; the result must be the f32 sum of compute.go:74-92 rounded
     once to the 16-bit format, i.e. the oracle's narrowing of numpy's exact integer
-    product.  The first shape takes the 8-wave 256 x 256 kernel, the others the
-    4-wave 128 x 128 one; all have ragged row and column tiles (the epilogue's
-    bounds) and K tails.  A misplaced, missing or duplicated element fails here,
+    product.  The first shape takes the 8-wave 256 x 256 kernel, the second the
+    4-wave 128 x 128 one, the others (under one round of 128 x 128 tiles) the
+    split-K kernel, unsplit, then in two chunks (1000 x 2048 x 520); all have
+    ragged row and column tiles (the epilogue's bounds) and K tails.  A misplaced, missing or duplicated element fails here,
     where a normwise bar could hide it."""
     rng = np.random.default_rng(rows + 7 * inner + 3 * cols)
     ai = rng.integers(-3, 4, (rows, inner))
@@ -80,11 +82,13 @@ def test_matmul_16bit_exact_integer_products(backend, dt, rows, inner, cols):
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("rows,inner,cols", [(64, 4096, 4096), (1, 4104, 2056), (200, 1000, 1024),
-                                             (256, 512, 14336), (3, 64, 8), (500, 1032, 4104), (256, 512, 1024)])
+                                             (256, 512, 14336), (3, 64, 8), (500, 1032, 4104), (256, 512, 1024),
+                                             (1000, 4096, 1000)])
 def test_matmul_16bit_skinny_split_k(backend, dt, rows, inner, cols):
     """rows <= 512 take the split-K kernel (64 x 128 tiles over chunks of K, f32
-    partials summed in chunk order): ragged rows / columns, K tails, one-chunk and
-    many-chunk splits; 200 x 1000 x 1024 (128 to 256 rows, a right operand of at
+    partials summed in chunk order), as do outputs under one round of 128 x 128
+    tiles (1000 x 4096 x 1000: four chunks of 1024): ragged rows / columns, K
+    tails, one-chunk and many-chunk splits; 200 x 1000 x 1024 (128 to 256 rows, a right operand of at
     most 2^22 elements) takes the small kernel instead, K split over the 8 waves of
     each block, on 16 x 16 tiles (as do 256x256x128 and 128x512x512 above), and
     256 x 512 x 1024 (256 tiles of 32 x 32) on 32 x 32 tiles.  Oracle rows sampled across the tile bands (all columns),
@@ -191,10 +195,10 @@ def test_matmul_k_tail_never_reads_the_next_row(backend):
 
 
 @pytest.mark.parametrize("rows,inner,cols,sample", [(4096, 72, 4096, [0, 2, 255, 256, 2047, 4095]),
-                                                    (1000, 72, 1032, [0, 2, 127, 128, 999])])
+                                                    (4000, 72, 4104, [0, 2, 127, 128, 2047, 3999])])
 def test_matmul_wide_k_tail_never_reads_the_next_row(backend, rows, inner, cols, sample):
     """The same isolation on the MFMA GEMM, 256 x 256 tiles (4096 x 4096) and
-    128 x 128 tiles (1000 x 1032, ragged): inner = 72 leaves 8 valid columns in the
+    128 x 128 tiles (4000 x 4104, ragged): inner = 72 leaves 8 valid columns in the
     last 64-wide slice; only output row 1 may be NaN."""
     a32 = seeded(903, (rows, inner))
     a32[1, 0] = np.nan
