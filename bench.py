@@ -468,12 +468,16 @@ def pages(torch, be, puter, return_fns=False):
 
 
 def matmul_bf16(torch, be, puter):
-    """Matmul in bf16 (f32 accumulation) on the MFMA GEMM: a square 8192^3, the
-    MLP up-projection shape rows 8192 x inner 4096 x cols 14336, and decode-step
-    projections of 64 rows (split-K path)."""
+    """Matmul in bf16 (f32 accumulation): a square 8192^3 and the MLP
+    up-projection shape rows 8192 x inner 4096 x cols 14336 (256 x 256 tiles),
+    6144 x 4096 x 4096 (128 x 128 tiles), 2048^3 and 1024 x 8192 x 1024 (under one
+    round of 128 x 128 tiles: the split-K kernel, unsplit and in four chunks), and
+    decode-step projections of 64 rows (split-K path)."""
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0006)
     res = {}
-    for name, (M, K, N) in (("8192c", (8192, 8192, 8192)), ("mlp", (8192, 4096, 14336))):
+    for name, (M, K, N) in (("8192c", (8192, 8192, 8192)), ("mlp", (8192, 4096, 14336)),
+                            ("m6144_k4096_n4096", (6144, 4096, 4096)), ("2048c", (2048, 2048, 2048)),
+                            ("m1024_k8192_n1024", (1024, 8192, 1024))):
         a = torch.randn(M * K, device="cuda", generator=gen).to(torch.bfloat16)
         b = torch.randn(K * N, device="cuda", generator=gen).to(torch.bfloat16)
         c = torch.empty(M * N, device="cuda", dtype=torch.bfloat16)

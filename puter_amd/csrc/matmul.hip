@@ -409,9 +409,11 @@ __global__ __launch_bounds__(128 * NW, NW == 4 ? 1 : 2) void matmul_mfma_kernel(
     // not re-read by this kernel): +2 to +7% on 8192^3, 8192 x 4096 x 14336 and 4096^3.
     // The wave owns HW 8 KB halves of the ring (64 rows of 128 bytes each: halves
     // HW w .. HW w + HW - 1, counted through the A buffers, then the B buffers); row r
-    // keeps its 16-byte chunk c (8 columns) at c ^ (r % 8), so the 8-byte writes (16
-    // rows per LDS cycle) and the 16-byte reads (one row per cycle) are free of bank
-    // conflicts.
+    // keeps its 16-byte chunk c (8 columns) at c ^ (r / 2 % 8), so 16 consecutive rows
+    // (r % 2 picking the half of the 256-byte bank line) and each row's 8 chunks fall
+    // on distinct banks.  Measured: 128 bank-conflict cycles per wave and tile (0 in
+    // the main loop), the same under c ^ (r % 8) and with the 8-byte halves also
+    // swizzled, so not this layout's; about 0.03% of a tile's time.
     {
         constexpr int HW = MT / 2, HA = A_BYTES / 8192, HB = B_BYTES / 8192;
         static_assert(S * (HA + HB) >= 2 * NW * HW, "the ring holds every wave's block");
@@ -441,7 +443,7 @@ __global__ __launch_bounds__(128 * NW, NW == 4 ? 1 : 2) void matmul_mfma_kernel(
                     uint32_t h[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) h[i] = Elem<DT>::store(acc[mt][nt][4 * rb + i]);
-                    const int chunk = (4 * nt + rb) ^ (l32 & 7);
+                    const int chunk = (4 * nt + rb) ^ ((l32 >> 1) & 7);
                     *reinterpret_cast<uint2 *>(hb + chunk * 16 + 8 * g) =
                         make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
                 }
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(128 * NW, NW == 4 ? 1 : 2) void matmul_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < WR / 8; ++i) {
             const int rr = 8 * (i & 7) + r8;   // row inside the half
-            const mm_u32x4 v = *reinterpret_cast<const mm_u32x4 *>(hs[i >> 3] + rr * 128 + ((c8 ^ (rr & 7)) << 4));
+            const mm_u32x4 v = *reinterpret_cast<const mm_u32x4 *>(hs[i >> 3] + rr * 128 + ((c8 ^ ((rr >> 1) & 7)) << 4));
             const int row = m0 + WR * wm + 8 * i + r8;
             if (row < M && col < N)   // N % 8 == 0: a chunk is wholly inside or outside
                 __builtin_nontemporal_store(v, reinterpret_cast<mm_u32x4 *>(p.c + (int64_t)row * N + col));
