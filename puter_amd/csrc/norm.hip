@@ -10,9 +10,8 @@
 //
 // Fast paths keep the row in registers, so every tensor is read once and
 // written once (for the fused op, 8 B/elem of HBM traffic in bf16):
-//   - norm_row_kernel: a block per row (two rows for the standalone norms at
-//     one vector per thread), one 16-byte vector per thread per tensor (long
-//     rows, many rows);
+//   - norm_row_kernel: a block per row, 1-8 16-byte vectors per thread per
+//     tensor (long rows, many rows);
 //   - norm_wave_kernel: one wave64 per row, 4 rows per 256-thread block, the row
 //     as VPL 16-byte vectors per lane (lane l owns vectors j*64 + l, so each
 //     wave-wide load is one contiguous 1 KiB burst); register-only butterflies.
@@ -228,19 +227,15 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
 }
 
 // ------------------------------------------------------- row-block path --
-// A block per R rows (R = 1 or 2), each row spread over the whole block: thread t
-// owns the V 16-byte vectors j*T + t of every row (T = blockDim.x, T*V*N = H), so
-// every tensor is still read once and written once, but each thread keeps only V
-// (1 for bf16 rows of up to 8192) loads of each input per row in flight.  Measured on
-// MI355X, this launch shape (many threads, one vector each) sustains ~10% more HBM
-// bandwidth on the 2-read / 2-write stream than a wave per row holding the row in
-// 4-16 vectors per lane.  The sums go through a wave butterfly and one LDS round (T/64
-// partials, one barrier per reduction, the R rows' sums side by side), so a row's sum
-// is taken in the same order whatever R is.  All R rows' loads are issued before the
-// first reduction: R = 2 doubles the bytes a block keeps in flight through its
-// barriers, which pays where a thread holds one vector of a row (standalone RMSNorm /
-// LayerNorm at 4096 bf16 columns, +7-9%, same process, bit-identical) and not where
-// the block already streams two vectors or the fused gated residual (-1 to -3%).
+// A block per R rows, each row spread over the whole block: thread t owns the V
+// 16-byte vectors j*T + t of every row (T = blockDim.x, T*V*N = H), so every tensor is
+// read once and written once, with V loads of each input per row in flight per
+// thread (launch_norm picks V per op).  The sums go through a wave butterfly and one
+// LDS round (T/64 partials, one barrier per reduction, the R rows' sums side by
+// side), so a row's sum is taken in the same order whatever R is.  Every launch uses
+// R = 1: two rows per block (all their loads issued before the first barrier) gained
+// 7-9% on the unfused norms at one vector per thread, but fewer threads per row with
+// more vectors each gained more (see launch_norm), and R = 2 lost 1-3% elsewhere.
 template <int DT, int OP, bool GR, int V, int R>
 __global__ __launch_bounds__(1024) void norm_row_kernel(NormArgs a) {
 #pragma clang fp contract(off)
@@ -486,27 +481,29 @@ static int launch_norm(const NormArgs &a, hipStream_t s, bool vec_ok) {
     constexpr int N = Vec<DT>::N;
     // Launch shape, chosen by same-process measurements on MI355X (bf16 sweep of
     // 1024 / 16384 / 65536 rows x 2048 / 4096 / 8192): with thousands of rows and
-    // rows of at least 512 16-byte vectors, a block per row (one vector per
-    // thread per tensor) streams 3-12% faster than a wave per row; the fused
-    // GatedResidual+RMSNorm does best at up to 1024 threads per row, norms with
-    // two reductions (LayerNorm, modulated) and the unfused norms at 512.  Fewer
-    // rows (latency-bound) and shorter rows keep the wave per row.
+    // rows of at least 512 16-byte vectors, a block per row streams 3-12% faster
+    // than the wave-per-row kernel.  The fused GatedResidual+RMSNorm does best at
+    // one vector per thread (up to 1024 threads), the fused LayerNorm at up to 512
+    // threads; the unfused norms with fewer threads and more vectors each: V = 2
+    // for RMSNorm (4096 columns: 5725 -> 5908 / 6015 -> 6201 GB/s at 16384 / 65536
+    // rows against V = 1), V = 8 for the two-reduction LayerNorm, whose barriers
+    // cost less over fewer waves (4096 columns, 64 threads: 4667 -> 5638 / 5014 ->
+    // 5999; 8192, 128 threads: 5352 -> 5659 / 5641 -> 5799 against 512 threads).
+    // Fewer rows (latency-bound) and shorter rows keep the wave per row.
     const int64_t U = a.H / N;
     constexpr bool two_pass = OP == OP_LN || OP == OP_MODULATED;
     if (vec_ok && a.H % (64 * N) == 0 && a.rows >= 4096 && U >= 512) {
-        const int64_t max_t = (GR && !two_pass) ? 1024 : 512;
-        int V = 1;
+        int64_t V = 1, max_t = 1024;
+        if constexpr (GR) max_t = two_pass ? 512 : 1024;
+        else V = two_pass ? 8 : 2;
         while (U / V > max_t) V *= 2;
-        if (V <= 4 && U % V == 0 && (U / V) % 64 == 0) {
+        if (V <= 8 && U % V == 0 && (U / V) % 64 == 0) {
             const unsigned T = (unsigned)(U / V), blocks = (unsigned)a.rows;
-            if (!GR && V == 1 && a.rows % 2 == 0) {
-                norm_row_kernel<DT, OP, GR, 1, 2><<<blocks / 2, T, 0, s>>>(a);
-                return check_launch("norm");
-            }
             switch (V) {
             case 1: norm_row_kernel<DT, OP, GR, 1, 1><<<blocks, T, 0, s>>>(a); break;
             case 2: norm_row_kernel<DT, OP, GR, 2, 1><<<blocks, T, 0, s>>>(a); break;
-            default: norm_row_kernel<DT, OP, GR, 4, 1><<<blocks, T, 0, s>>>(a); break;
+            case 4: norm_row_kernel<DT, OP, GR, 4, 1><<<blocks, T, 0, s>>>(a); break;
+            default: norm_row_kernel<DT, OP, GR, 8, 1><<<blocks, T, 0, s>>>(a); break;
             }
             return check_launch("norm");
         }
