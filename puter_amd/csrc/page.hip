@@ -251,7 +251,13 @@ __global__ __launch_bounds__(256) void page_gather_kernel(const char *__restrict
         return;
     }
     const V *src = reinterpret_cast<const V *>(storage) + ((int64_t)id * page_size + row % page_size) * row_units;
-    for (int64_t u = lane; u < row_units; u += 64) dst[u] = src[u];
+    // the gathered rows are read and written once here: non-temporal 16-byte
+    // accesses (configs[4]'s pool, 290,592 rows of 2 KiB: 224.9 -> 193.5 us, 5.29 ->
+    // 6.15 TB/s; issuing a lane's loads of the row before its stores gained nothing)
+    for (int64_t u = lane; u < row_units; u += 64) {
+        if constexpr (sizeof(V) == 16) st_stream(ld_stream(src + u), dst + u);
+        else dst[u] = src[u];
+    }
 }
 
 // One block per R rows (rows_per_block, a power of two; dynamic LDS of
@@ -302,7 +308,11 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(8))) vo
         if (q >= total) return;
         const int64_t i = unit_shift >= 0 ? q >> unit_shift : q / row_units;
         if (!write_wins(t, (int)i)) return;
-        dst[write_slot(t, (int)i, page_size) * row_units + (q - i * row_units)] = v;
+        V *const p = &dst[write_slot(t, (int)i, page_size) * row_units + (q - i * row_units)];
+        // non-temporal 16-byte stores (the pool rows are not re-read here): 16384 / 65536
+        // rows of 2 KiB 13.0 -> 12.3 / 54.0 -> 47.4 us; non-temporal value loads lost
+        if constexpr (sizeof(V) == 16) st_stream(v, p);
+        else *p = v;
     };
     put(tid, v0);
     put(tid + B, v1);
