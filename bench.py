@@ -22,6 +22,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3   # dense f32 MFMA (and vector) peak
 ROWS = (1024, 16384, 65536)
 HIDDEN = (2048, 4096, 8192)
 
@@ -467,12 +468,13 @@ def pages(torch, be, puter, return_fns=False):
     return res
 
 
-def matmul_bf16(torch, be, puter):
+def matmul_legs(torch, be, puter):
     """Matmul in bf16 (f32 accumulation): a square 8192^3 and the MLP
     up-projection shape rows 8192 x inner 4096 x cols 14336 (256 x 256 tiles),
     6144 x 4096 x 4096 (128 x 128 tiles), 2048^3 and 1024 x 8192 x 1024 (under one
     round of 128 x 128 tiles: the split-K kernel, unsplit and in four chunks), and
-    decode-step projections of 64 rows (split-K path)."""
+    decode-step projections of 64 rows (split-K path); in f32 (the reference's default
+    format) 4096^3 and the MLP shape on the f32 MFMA kernel."""
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0006)
     res = {}
     for name, (M, K, N) in (("8192c", (8192, 8192, 8192)), ("mlp", (8192, 4096, 14336)),
@@ -491,6 +493,24 @@ def matmul_bf16(torch, be, puter):
         t = Timer(torch).time(lambda: torch.matmul(a2, b2), 10, warmup=3)
         res[f"context_torch_matmul_bf16_{name}_TFLOPs"] = round(2.0 * M * K * N / (t * 1e-3) / 1e12, 1)
         del a, b, c, a2, b2
+    # f32 (the reference's default format) on the f32 MFMA kernel; context: torch.matmul
+    # in f32 with TF32 off
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for name, (M, K, N) in (("4096c", (4096, 4096, 4096)), ("mlp", (8192, 4096, 14336))):
+        a = torch.randn(M * K, device="cuda", generator=gen)
+        b = torch.randn(K * N, device="cuda", generator=gen)
+        c = torch.empty(M * N, device="cuda")
+        t = Timer(torch).time(lambda: be.Matmul(c, a, b, M, K, N, puter.F32), 10, warmup=3)
+        tf = 2.0 * M * K * N / (t * 1e-3) / 1e12
+        res[f"matmul_f32_{name}_ms"] = round(t, 3)
+        res[f"matmul_f32_{name}_TFLOPs"] = round(tf, 1)
+        res[f"matmul_f32_{name}_frac"] = round(tf / F32_PEAK_TFLOPS, 4)
+        a2, b2 = a.view(M, K), b.view(K, N)
+        t = Timer(torch).time(lambda: torch.matmul(a2, b2), 10, warmup=3)
+        res[f"context_torch_matmul_f32_{name}_TFLOPs"] = round(2.0 * M * K * N / (t * 1e-3) / 1e12, 1)
+        del a, b, c, a2, b2
+    torch.backends.cuda.matmul.allow_tf32 = tf32
     # decode-step projections (batch 64 rows against a weight matrix): HBM-bound,
     # GB/s of operand + output bytes
     for M, K, N in ((64, 4096, 4096), (64, 4096, 14336), (64, 14336, 4096)):
@@ -922,7 +942,7 @@ def main():
         log(f"pages: write 16384 rows {configs['page_write_prefill_16384_GBs']} GB/s, "
             f"gather {configs['page_gather_b64_GBs']} GB/s")
     if "matmul" in only:
-        configs.update(matmul_bf16(torch, be, puter))
+        configs.update(matmul_legs(torch, be, puter))
         log(f"matmul bf16: {configs['matmul_bf16_8192c_TFLOPs']} TFLOP/s at 8192^3")
     if "block" in only:
         configs.update(block_f32(torch, be, puter))

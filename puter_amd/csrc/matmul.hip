@@ -487,6 +487,189 @@ static int launch_mfma(void *out, const void *left, const void *right, int64_t M
     return 0;
 }
 
+// ---------------------------------------------------------- f32 MFMA --
+// Large f32 outputs on v_mfma_f32_32x32x2_f32 (exact f32 products, f32 sums).  A
+// 256-thread block (4 waves, 2 x 2) computes a 128 x 128 tile, K advancing 32 at a
+// time through LDS (double buffered; slices copied HBM -> LDS by buffer_load ... lds),
+// two blocks per CU.  Wave (wm, wn) owns rows 64 wm .. +63 and columns 64 wn .. +63
+// as 2 x 2 accumulators; a lane's accumulator holds C[8 (r/4) + 4 h + r%4][lane % 32]
+// of its 32 x 32 block (h = lane / 32).  k order: MFMA step s (0..15) of a slice
+// gives half h of the wave k = 8 (s / 4) + 4 h + s % 4 (an MFMA may pair its two k's
+// in any order, as long as A and B agree), so a lane's A operands for four steps are
+// one 16-byte run of its row.  LDS layouts: the A slice keeps rows of 32 floats (128
+// bytes) with 16-byte chunk c of row r at c ^ (r / 2 % 8), so the 16 rows an LDS
+// cycle serves fall on distinct banks; the B slice keeps rows of 128 floats (512
+// bytes) with chunk c of row k at c ^ 8 (k / 4 % 2), so the two half-waves (rows k
+// and k + 4, one float per lane) read opposite halves of the bank line.  Rows past
+// M or K arrive as zeros through the buffer ranges, and in the last slice A chunks
+// past K as well (the next row's values must not meet B's zero rows: 0 * Inf would
+// be NaN); columns past N are computed from whatever follows and never stored.
+// Requirements: K % 4 == 0, N % 4 == 0, 16-byte aligned buffers.
+namespace mf {
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int RA = BK * 4, RB = BN * 4;              // LDS row bytes: 128, 512
+constexpr int A_BYTES = BM * RA, B_BYTES = BK * RB;  // 16 KB each
+}  // namespace mf
+
+struct MfArgs {
+    const float *a, *b;
+    float *c;
+    int M, N, K;
+    int tiles_m, tiles_n, groups_m;
+};
+
+typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256, 2) void matmul_f32_mfma_kernel(MfArgs p) {
+    using namespace mf;
+    using mm::OOB;
+    using mm::BUF_WORD3;
+    __shared__ __attribute__((aligned(1024))) char as0[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char as1[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char bs0[B_BYTES];
+    __shared__ __attribute__((aligned(1024))) char bs1[B_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // block -> output tile: XCD x runs the 4 x 8 tile groups x, x + 8, ... (as the
+    // 16-bit kernel), so the blocks an XCD runs at once share A and B panels in its L2
+    const int id = blockIdx.x;
+    const int local = id >> 3, grp = (local >> 5) * 8 + (id & 7), w = local & 31;
+    const int tm = (grp % p.groups_m) * 4 + (w & 3);
+    const int tn = (grp / p.groups_m) * 8 + (w >> 2);
+    if (tm >= p.tiles_m || tn >= p.tiles_n) return;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int M = p.M, N = p.N, K = p.K;
+
+    // copy offsets (bytes from the slice's descriptor base).  A: copy i of wave w
+    // fills rows 32 w + 8 i .. +7 (lane: row + lane / 8, LDS chunk lane % 8, holding
+    // the row's chunk (lane % 8) ^ swizzle); B: rows 8 w + 2 i, +1 (lane: row + lane
+    // / 32, LDS chunk lane % 32)
+    int aoff[4], achunk[4], boff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ra = 32 * wave + 8 * i + (lane >> 3);
+        achunk[i] = (lane & 7) ^ ((ra >> 1) & 7);
+        aoff[i] = ra * K * 4 + achunk[i] * 16;
+        const int rb = 8 * wave + 2 * i + (lane >> 5);
+        boff[i] = rb * N * 4 + (((lane & 31) ^ (8 * ((rb >> 2) & 1))) << 4);
+    }
+    // operand reads: A row 64 wm + 32 mt + l32, 4-step group g at chunk (2 g + h) ^
+    // swizzle; B column 64 wn + 32 nt + l32 of row k, stored at column ^ 32 h (k / 4 % 2
+    // = h for every k a half-wave reads)
+    const int asw = (l32 >> 1) & 7;
+    int ard[2], brd[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) ard[mt] = (64 * wm + 32 * mt + l32) * RA;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) brd[nt] = (((64 * wn + 32 * nt + l32) ^ (32 * h)) << 2) + 4 * h * RB;
+
+    const int64_t a_rows_bytes = (int64_t)(M - m0) * K * 4;
+    auto copy_slice = [&](int k0, char *as, char *bs) __attribute__((always_inline)) {
+        const int64_t abase = (int64_t)m0 * K + k0;
+        const int64_t arange = std::min<int64_t>(a_rows_bytes - (int64_t)k0 * 4, OOB);
+        const __amdgpu_buffer_rsrc_t ad =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(p.a + abase), (short)0, (int)arange, BUF_WORD3);
+        const int64_t bbase = (int64_t)k0 * N + n0;
+        const int64_t brange = std::min<int64_t>(((int64_t)K * N - bbase) * 4, OOB);
+        const __amdgpu_buffer_rsrc_t bd =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(p.b + bbase), (short)0, (int)brange, BUF_WORD3);
+        const bool tail = k0 + BK > K;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int off = (tail && k0 + 4 * achunk[i] >= K) ? OOB : aoff[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ad, (mm_lds_void *)(as + (32 * wave + 8 * i) * RA), 16, off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bd, (mm_lds_void *)(bs + (8 * wave + 2 * i) * RB), 16, boff[i], 0, 0, 0);
+    };
+
+    mm_f32x16 acc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = (mm_f32x16){};
+
+    auto compute = [&](const char *as, const char *bs) __attribute__((always_inline)) {
+#pragma unroll
+        for (int g = 0; g < BK / 8; ++g) {
+            mf_f32x4 av[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+                av[mt] = *reinterpret_cast<const mf_f32x4 *>(as + ard[mt] + (((2 * g + h) ^ asw) << 4));
+            float bv[2][4];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    bv[nt][s] = *reinterpret_cast<const float *>(bs + brd[nt] + (8 * g + s) * RB);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[mt][s], bv[nt][s], acc[mt][nt], 0, 0, 0);
+        }
+    };
+
+    const int nk = (K + BK - 1) / BK;
+    copy_slice(0, as0, bs0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    auto slice = [&](int kt, char *ac, char *bc, char *an, char *bn) __attribute__((always_inline)) {
+        if (kt + 1 < nk) copy_slice((kt + 1) * BK, an, bn);
+        __builtin_amdgcn_sched_barrier(0);   // keep the copies ahead of the compute
+        compute(ac, bc);
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        slice(kt, as0, bs0, as1, bs1);
+        slice(kt + 1, as1, bs1, as0, bs0);
+    }
+    if (kt < nk) slice(kt, as0, bs0, as1, bs1);
+
+    // lane writes C[row][n0 + 64 wn + 32 nt + l32]: 32 consecutive floats of a row
+    // per half-wave and register
+    const int col0 = n0 + 64 * wn + l32;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + 64 * wm + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row >= M) continue;
+            float *crow = p.c + (int64_t)row * N;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+                if (col0 + 32 * nt < N) __builtin_nontemporal_store(acc[mt][nt][r], crow + col0 + 32 * nt);
+        }
+}
+
+// Launches the f32 MFMA kernel; returns 1 when the shape does not fit it.
+static int launch_f32_mfma(float *out, const float *left, const float *right, int64_t M, int64_t K, int64_t N,
+                           hipStream_t s) {
+    if (K % 4 || N % 4 || !aligned16(out) || !aligned16(left) || !aligned16(right)) return 1;
+    if (128 * K * 4 >= mm::OOB || mf::BK * N * 4 >= mm::OOB || M > 0x3FFFFFFF || N > 0x3FFFFFFF) return 1;
+    MfArgs p;
+    p.a = left;
+    p.b = right;
+    p.c = out;
+    p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    p.tiles_m = (int)((M + mf::BM - 1) / mf::BM);
+    p.tiles_n = (int)((N + mf::BN - 1) / mf::BN);
+    p.groups_m = (p.tiles_m + 3) / 4;
+    const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
+    const int64_t blocks = (groups + 7) / 8 * 8 * 32;
+    if (blocks > 0x7FFFFFFF) return 1;
+    matmul_f32_mfma_kernel<<<(unsigned)blocks, 256, 0, s>>>(p);
+    return check_launch("matmul f32 mfma");
+}
+
 // ------------------------------------------------ small outputs, 16-bit --
 // The 16-bit counterpart of matmul_f32_small_kernel: one 512-thread block per
 // TM x TM output tile, its 8 waves splitting K into runs of kw (a multiple of
@@ -1012,6 +1195,13 @@ __global__ __launch_bounds__(256) void matmul_splitk_reduce_f32_kernel(float *c,
 // computing: 128x512x512 18.3 -> 12.9 us), partials in the split-K scratch.
 static int launch_matmul_f32(float *out, const float *left, const float *right, int64_t M, int64_t K, int64_t N,
                              hipStream_t s, PartialsTarget tgt) {
+#ifndef F32_MFMA_MIN_TILES
+#define F32_MFMA_MIN_TILES 256
+#endif
+    if (((M + 127) / 128) * ((N + 127) / 128) >= F32_MFMA_MIN_TILES && K >= 64) {
+        const int rc = launch_f32_mfma(out, left, right, M, K, N, s);
+        if (rc != 1) return rc;
+    }
     const dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
     if (grid.y > 65535) return fail(PUTER_ERR_INVALID, "matmul: too many rows");
     const int64_t tiles = (int64_t)grid.x * grid.y, steps = (K + kDepth - 1) / kDepth;

@@ -80,6 +80,46 @@ def test_matmul_16bit_exact_integer_products(backend, dt, rows, inner, cols):
     assert bad.size == 0, f"{bad.shape[0]} cells differ, e.g. {bad[:4].tolist()}: {got[tuple(bad[:4].T)]} vs {want[tuple(bad[:4].T)]}"
 
 
+@pytest.mark.parametrize("rows,inner,cols", [(4000, 264, 4104), (2048, 100, 2052), (2100, 64, 2048)])
+def test_matmul_f32_exact_integer_products(backend, rows, inner, cols):
+    """F32 outputs of at least 256 tiles of 128 x 128 take the f32 MFMA kernel: small
+    integer operands keep every partial sum exact in f32 whatever the summation
+    order, so every output must equal numpy's exact integer product bit for bit
+    (ragged row and column tiles, K tails of 8 and 4, K of exactly two slices).
+    NaN-poisoned output: a missing, misplaced or duplicated element fails."""
+    rng = np.random.default_rng(rows + 7 * inner + 3 * cols)
+    ai = rng.integers(-3, 4, (rows, inner)).astype(np.float32)
+    bi = rng.integers(-2, 3, (inner, cols)).astype(np.float32)
+    want = (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32)
+    out = empty_dev((rows, cols), np.float32)
+    out.fill_(float("nan"))
+    backend.Matmul(out, to_dev(ai), to_dev(bi), rows, inner, cols, O.F32)
+    got = to_host(out, np.float32)
+    bad = np.argwhere(got.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, f"{bad.shape[0]} cells differ, e.g. {bad[:4].tolist()}: {got[tuple(bad[:4].T)]} vs {want[tuple(bad[:4].T)]}"
+
+
+def test_matmul_f32_mfma_k_tail_never_reads_the_next_row(backend):
+    """The f32 MFMA kernel's last 32-deep slice holds 4 valid columns (inner = 68);
+    the chunks past inner must arrive as zeros, not as the next row's first values.
+    Row 1 of `left` starts with NaN: only output row 1 may be NaN, and the rest
+    matches the oracle."""
+    rows, inner, cols = 2048, 68, 2048
+    a = seeded(907, (rows, inner))
+    a[1, 0] = np.nan
+    b = seeded(908, (inner, cols), 0.0, 0.05)
+    out = empty_dev((rows, cols), np.float32)
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, O.F32)
+    got = to_host(out, np.float32)
+    assert np.isnan(got[1]).all()
+    keep = np.ones(rows, bool)
+    keep[1] = False
+    assert np.isfinite(got[keep]).all()
+    sample = [0, 2, 127, 128, 1023, 2047]
+    ref = O.matmul(np.ascontiguousarray(a[sample]), b, O.F32)
+    assert_close(got[sample], ref, TOL[O.F32], elem_tol=None, what="f32 mfma k tail")
+
+
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("rows,inner,cols", [(64, 4096, 4096), (1, 4104, 2056), (200, 1000, 1024),
                                              (256, 512, 14336), (3, 64, 8), (500, 1032, 4104), (256, 512, 1024),
