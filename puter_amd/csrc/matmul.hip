@@ -37,12 +37,14 @@
 // buffers, 256 * K * 2 and BK * N * 2 below 2^31; other shapes take the generic
 // kernel (one thread per output, f32 accumulation in index order).
 //
-// f32: 64 x 64 output tile per 256-thread block, 16-deep K slices in LDS, 4 x 4
-// register micro-tile, f32 FMA; grids of fewer than 256 tiles take the small
-// kernel (32 x 32 tiles, K split over the 8 waves of each block on the f32 MFMA)
-// when K is short for the tile count, else split K across blocks (f32 partials
-// summed in chunk order).  f64: one thread per output, f64 sum in index
-// order (matmulFloat64Scalar, device/cpu/matmul/select_generic.go:39-...).
+// f32: small outputs of moderate depth take the small kernel (32 x 32 or 16 x 16
+// tiles, K split over the 8 waves of each block on the f32 MFMA); other shapes with K
+// and N multiples of 4 and 16-byte aligned buffers the f32 MFMA kernel (128 x 128
+// tiles, v_mfma_f32_32x32x2_f32, K split across blocks for grids of fewer tiles than
+// CUs); the rest a VALU kernel (64 x 64 tile per 256-thread block, 16-deep K slices in
+// LDS, 4 x 4 register micro-tile, f32 FMA; K split across blocks for small grids).
+// Split K always sums the f32 partials in chunk order.  f64: one thread per output,
+// f64 sum in index order (matmulFloat64Scalar, device/cpu/matmul/select_generic.go:39-...).
 #include "common.hpp"
 #include <algorithm>
 #include <atomic>
@@ -514,8 +516,11 @@ constexpr int A_BYTES = BM * RA, B_BYTES = BK * RB;  // 16 KB each
 struct MfArgs {
     const float *a, *b;
     float *c;
+    float *ws;  // split K: [chunks][M][N] partials (chunk = blockIdx.y), or null
     int M, N, K;
+    int kc;     // K per chunk (a multiple of 32; K when unsplit)
     int tiles_m, tiles_n, groups_m;
+    int grouped;  // XCD-grouped tile order (else block x = tile, row-major)
 };
 
 typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
@@ -533,15 +538,25 @@ __global__ __launch_bounds__(256, 2) void matmul_f32_mfma_kernel(MfArgs p) {
     const int l32 = lane & 31, h = lane >> 5;
     const int wm = wave >> 1, wn = wave & 1;
 
-    // block -> output tile: XCD x runs the 4 x 8 tile groups x, x + 8, ... (as the
-    // 16-bit kernel), so the blocks an XCD runs at once share A and B panels in its L2
+    // block -> output tile.  Grouped: XCD x runs the 4 x 8 tile groups x, x + 8, ...
+    // (as the 16-bit kernel), so the blocks an XCD runs at once share A and B panels in
+    // its L2.  Grids of fewer tiles than CUs (split K) number the tiles plainly: the
+    // grouped order would put a grid of one group on a single XCD (32 x 8192 x 1024,
+    // 8 tiles in 16 chunks: 497 us)
     const int id = blockIdx.x;
-    const int local = id >> 3, grp = (local >> 5) * 8 + (id & 7), w = local & 31;
-    const int tm = (grp % p.groups_m) * 4 + (w & 3);
-    const int tn = (grp / p.groups_m) * 8 + (w >> 2);
-    if (tm >= p.tiles_m || tn >= p.tiles_n) return;
+    int tm, tn;
+    if (p.grouped) {
+        const int local = id >> 3, grp = (local >> 5) * 8 + (id & 7), w = local & 31;
+        tm = (grp % p.groups_m) * 4 + (w & 3);
+        tn = (grp / p.groups_m) * 8 + (w >> 2);
+        if (tm >= p.tiles_m || tn >= p.tiles_n) return;
+    } else {
+        tm = id / p.tiles_n;
+        tn = id - tm * p.tiles_n;
+    }
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.M, N = p.N, K = p.K;
+    const int kb = blockIdx.y * p.kc, ke = min(K, kb + p.kc);   // this block's K range
 
     // copy offsets (bytes from the slice's descriptor base).  A: copy i of wave w
     // fills rows 32 w + 8 i .. +7 (lane: row + lane / 8, LDS chunk lane % 8, holding
@@ -616,12 +631,12 @@ __global__ __launch_bounds__(256, 2) void matmul_f32_mfma_kernel(MfArgs p) {
         }
     };
 
-    const int nk = (K + BK - 1) / BK;
-    copy_slice(0, as0, bs0);
+    const int nk = (ke - kb + BK - 1) / BK;
+    copy_slice(kb, as0, bs0);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     auto slice = [&](int kt, char *ac, char *bc, char *an, char *bn) __attribute__((always_inline)) {
-        if (kt + 1 < nk) copy_slice((kt + 1) * BK, an, bn);
+        if (kt + 1 < nk) copy_slice(kb + (kt + 1) * BK, an, bn);
         __builtin_amdgcn_sched_barrier(0);   // keep the copies ahead of the compute
         compute(ac, bc);
         __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -635,39 +650,24 @@ __global__ __launch_bounds__(256, 2) void matmul_f32_mfma_kernel(MfArgs p) {
     if (kt < nk) slice(kt, as0, bs0, as1, bs1);
 
     // lane writes C[row][n0 + 64 wn + 32 nt + l32]: 32 consecutive floats of a row
-    // per half-wave and register
+    // per half-wave and register (non-temporal for the result; the partials of a
+    // split stay cacheable for the reduce that follows)
     const int col0 = n0 + 64 * wn + l32;
+    float *const cbase = p.ws ? p.ws + (int64_t)blockIdx.y * M * N : p.c;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = m0 + 64 * wm + 32 * mt + 8 * (r >> 2) + 4 * h + (r & 3);
             if (row >= M) continue;
-            float *crow = p.c + (int64_t)row * N;
+            float *crow = cbase + (int64_t)row * N;
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-                if (col0 + 32 * nt < N) __builtin_nontemporal_store(acc[mt][nt][r], crow + col0 + 32 * nt);
+            for (int nt = 0; nt < 2; ++nt) {
+                if (col0 + 32 * nt >= N) continue;
+                if (p.ws) crow[col0 + 32 * nt] = acc[mt][nt][r];
+                else __builtin_nontemporal_store(acc[mt][nt][r], crow + col0 + 32 * nt);
+            }
         }
-}
-
-// Launches the f32 MFMA kernel; returns 1 when the shape does not fit it.
-static int launch_f32_mfma(float *out, const float *left, const float *right, int64_t M, int64_t K, int64_t N,
-                           hipStream_t s) {
-    if (K % 4 || N % 4 || !aligned16(out) || !aligned16(left) || !aligned16(right)) return 1;
-    if (128 * K * 4 >= mm::OOB || mf::BK * N * 4 >= mm::OOB || M > 0x3FFFFFFF || N > 0x3FFFFFFF) return 1;
-    MfArgs p;
-    p.a = left;
-    p.b = right;
-    p.c = out;
-    p.M = (int)M; p.N = (int)N; p.K = (int)K;
-    p.tiles_m = (int)((M + mf::BM - 1) / mf::BM);
-    p.tiles_n = (int)((N + mf::BN - 1) / mf::BN);
-    p.groups_m = (p.tiles_m + 3) / 4;
-    const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
-    const int64_t blocks = (groups + 7) / 8 * 8 * 32;
-    if (blocks > 0x7FFFFFFF) return 1;
-    matmul_f32_mfma_kernel<<<(unsigned)blocks, 256, 0, s>>>(p);
-    return check_launch("matmul f32 mfma");
 }
 
 // ------------------------------------------------ small outputs, 16-bit --
@@ -1189,19 +1189,64 @@ __global__ __launch_bounds__(256) void matmul_splitk_reduce_f32_kernel(float *c,
     }
 }
 
-// f32: 64 x 64 tiles; grids of fewer than 256 tiles take the small kernel or split K (16-deep steps) into as
-// many chunks as keep the grid within 512 blocks, each chunk at least two steps
-// deep (one-step chunks spent more time writing and summing partials than
+// Launches the f32 MFMA kernel over `chunks` K chunks (f32 partials in the scratch,
+// summed in chunk order, when more than one); returns 1 when the shape does not fit it.
+static int launch_f32_mfma(float *out, const float *left, const float *right, int64_t M, int64_t K, int64_t N,
+                           int64_t chunks, hipStream_t s, PartialsTarget tgt) {
+    if (K % 4 || N % 4 || !aligned16(out) || !aligned16(left) || !aligned16(right)) return 1;
+    if (128 * K * 4 >= mm::OOB || mf::BK * N * 4 >= mm::OOB || M > 0x3FFFFFFF || N > 0x3FFFFFFF) return 1;
+    MfArgs p;
+    p.a = left;
+    p.b = right;
+    p.c = out;
+    p.ws = nullptr;
+    p.M = (int)M; p.N = (int)N; p.K = (int)K;
+    const int64_t slices = (K + mf::BK - 1) / mf::BK;
+    const int64_t per = (slices + chunks - 1) / chunks;   // slices per chunk
+    chunks = (slices + per - 1) / per;
+    p.kc = (int)(per * mf::BK);
+    p.tiles_m = (int)((M + mf::BM - 1) / mf::BM);
+    p.tiles_n = (int)((N + mf::BN - 1) / mf::BN);
+    p.groups_m = (p.tiles_m + 3) / 4;
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    const int64_t groups = (int64_t)p.groups_m * ((p.tiles_n + 7) / 8);
+    p.grouped = tiles >= device_cus();
+    const int64_t blocks = p.grouped ? (groups + 7) / 8 * 8 * 32 : tiles;
+    if (blocks > 0x7FFFFFFF) return 1;
+    const dim3 grid((unsigned)blocks, (unsigned)chunks);
+    if (chunks == 1) {
+        matmul_f32_mfma_kernel<<<grid, 256, 0, s>>>(p);
+        return check_launch("matmul f32 mfma");
+    }
+    const size_t need = (size_t)(chunks * M * N) * sizeof(float);
+    auto launch = [&](float *ws) {
+        p.ws = ws;
+        matmul_f32_mfma_kernel<<<grid, 256, 0, s>>>(p);
+        matmul_splitk_reduce_f32_kernel<<<(unsigned)std::min<int64_t>((M * N + 255) / 256, 4096), 256, 0, s>>>(
+            out, ws, M * N, (int)chunks);
+        return check_launch("matmul f32 mfma split-k");
+    };
+    if (tgt.fixed) {
+        if (need > noalloc::kScratchBytes)
+            return fail(PUTER_ERR_INVALID, "matmul (no-alloc): split-K partials of %zu bytes exceed the %zu-byte scratch",
+                        need, noalloc::kScratchBytes);
+        return launch(tgt.fixed);
+    }
+    ScratchLease lease(need, s);
+    if (lease.status()) return lease.status();
+    const int rc = launch(static_cast<float *>(lease.ptr()));
+    const int fin = lease.finish();
+    return rc ? rc : fin;
+}
+
+// f32: small outputs of moderate depth take the small kernel; other shapes with K and
+// N multiples of 4 and 16-byte aligned buffers the f32 MFMA kernel; the rest the VALU
+// kernel (64 x 64 tiles), whose grids of fewer than 256 tiles split K (16-deep steps)
+// into as many chunks as keep the grid within 512 blocks, each chunk at least two
+// steps deep (one-step chunks spent more time writing and summing partials than
 // computing: 128x512x512 18.3 -> 12.9 us), partials in the split-K scratch.
 static int launch_matmul_f32(float *out, const float *left, const float *right, int64_t M, int64_t K, int64_t N,
                              hipStream_t s, PartialsTarget tgt) {
-#ifndef F32_MFMA_MIN_TILES
-#define F32_MFMA_MIN_TILES 256
-#endif
-    if (((M + 127) / 128) * ((N + 127) / 128) >= F32_MFMA_MIN_TILES && K >= 64) {
-        const int rc = launch_f32_mfma(out, left, right, M, K, N, s);
-        if (rc != 1) return rc;
-    }
     const dim3 grid((unsigned)((N + kTile - 1) / kTile), (unsigned)((M + kTile - 1) / kTile));
     if (grid.y > 65535) return fail(PUTER_ERR_INVALID, "matmul: too many rows");
     const int64_t tiles = (int64_t)grid.x * grid.y, steps = (K + kDepth - 1) / kDepth;
@@ -1223,6 +1268,21 @@ static int launch_matmul_f32(float *out, const float *left, const float *right, 
             else matmul_f32_small_kernel<32, false><<<g32, 512, 0, s>>>(out, left, right, M, K, N, kw);
         }
         return check_launch("matmul");
+    }
+    // the f32 MFMA kernel (128 x 128 tiles, two blocks per CU).  Grids of fewer tiles
+    // than CUs split K into chunks (at least 256 deep, at most 16) toward two blocks
+    // per CU, f32 partials summed in order (1024 x 8192 x 1024: 13.5 -> 107 TFLOP/s
+    // against the VALU kernel, 1024^3 12 -> 56, 512 x 4096 x 4096 28 -> 105);
+    // splitting grids of a half round or more lost (2048^3 117 unsplit, 109 in two
+    // chunks), and aiming at one block per CU lost where few chunks remain (1536^3 63
+    // against 72-82, 128 x 8192 x 8192 101 against 111)
+    if (K >= 64) {
+        const int64_t cus = device_cus(), t128 = ((M + 127) / 128) * ((N + 127) / 128);
+        int64_t mchunks = 1;
+        if (t128 < cus)
+            mchunks = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>((2 * cus + t128 - 1) / t128, 16), K / 256));
+        const int rc = launch_f32_mfma(out, left, right, M, K, N, mchunks, s, tgt);
+        if (rc != 1) return rc;
     }
     int64_t chunks = tiles < 256 ? std::max<int64_t>(std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(512 / tiles, 1), steps / 2), 64), 1) : 1;
     const int64_t per = (steps + chunks - 1) / chunks;

@@ -267,16 +267,17 @@ def test_matmul_f64_and_f32(backend):
 
 @pytest.mark.parametrize("rows,inner,cols", [(128, 512, 512), (100, 1000, 300), (64, 96, 48), (7, 13, 5),
                                              (300, 40, 1100), (200, 333, 250), (32, 8192, 1024),
-                                             (256, 1024, 1024)])
+                                             (256, 1024, 1024), (33, 4100, 1030)])
 def test_matmul_f32_split_k(backend, rows, inner, cols):
     """F32 (config 1's Matmul): small outputs of moderate depth (at least 32 32x32
     tiles and few 64-deep steps per wave: 128x512x512, 100x1000x300, 200x333x250
     with unaligned A rows on 16 x 16 tiles, 256x1024x1024 on 32 x 32 tiles) split
-    K across the 8 waves of a block on the f32 MFMA;
-    other grids of fewer than 256 64x64 tiles (64x96x48, 32x8192x1024: too deep
-    for its 32 tiles) split K across blocks into 16-deep-step chunks summed in
-    order; ragged shapes and K tails, against the oracle's index-order f32 sum
-    at the f32 bar, and two calls bit-identical."""
+    K across the 8 waves of a block on the f32 MFMA; other aligned shapes take the
+    128 x 128 f32 MFMA kernel, 64x96x48 in one block, 32x8192x1024 (8 tiles) with K
+    split into 16 chunks summed in order; unaligned ones the VALU kernel, 33x4100x1030
+    (cols not a multiple of 4) with K split across blocks into 16-deep-step chunks;
+    ragged shapes and K tails, against the oracle's index-order f32 sum at the f32
+    bar, and two calls bit-identical."""
     a = seeded(rows * 5 + inner, (rows, inner))
     b = seeded(cols * 3 + inner, (inner, cols), 0.0, 0.05)
     ref = O.matmul_f32(a, b)
