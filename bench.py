@@ -286,8 +286,8 @@ def rope_swiglu_casts(torch, be, puter):
 
 
 def prefill(torch, be, puter, return_fn=False):
-    """causal GQA prefill bf16, B4 S4096 Hq32 Hkv8 D128 (return_fn:
-    only build the inputs and return the launch)."""
+    """causal GQA prefill bf16, B4 S4096 Hq32 Hkv8 D128, and the same
+    step in f32 at S2048 (return_fn: only build the bf16 inputs and return the launch)."""
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0003)
     B, S, H, KV, D = 4, 4096, 32, 8, 128
     sc = 1.0 / math.sqrt(D)
@@ -322,6 +322,21 @@ def prefill(torch, be, puter, return_fn=False):
         del qt, kt, vt
     except (RuntimeError, ImportError) as ex:
         log(f"torch flash SDPA unavailable: {ex}")
+    del q, k, v, o
+    # the same step in f32 (the reference's default format) at half the sequence, on
+    # the f32 MFMA prefill kernel
+    S2 = 2048
+    q = torch.randn(B * S2 * H * D, device="cuda", generator=gen) * sc
+    k = torch.randn(B * S2 * KV * D, device="cuda", generator=gen) * sc
+    v = torch.randn(B * S2 * KV * D, device="cuda", generator=gen)
+    o = torch.empty_like(q)
+    fn32 = lambda: be.MultiHeadAttentionBatched(cfg, q, k, v, o, B, S2, S2, puter.F32)  # noqa: E731
+    fn32()
+    t = Timer(torch).time(fn32, 10, warmup=5)
+    flops = 4.0 * B * H * D * S2 * (S2 + 1) / 2
+    tf = flops / (t * 1e-3) / 1e12
+    res.update({"prefill_f32_s2048_ms": round(t, 3), "prefill_f32_s2048_TFLOPs": round(tf, 1),
+                "prefill_f32_s2048_frac": round(tf / F32_PEAK_TFLOPS, 4)})
     del q, k, v, o
     torch.cuda.empty_cache()
     return res

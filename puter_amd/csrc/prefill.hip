@@ -88,6 +88,7 @@ template <> struct PfFormat<PUTER_F16> {
     using V4 = f16x4;
 };
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 namespace fa {
@@ -641,7 +642,276 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     }
 }
 
+// ------------------------------------------------------------ f32 prefill --
+// f32 MultiHeadAttention (head dim 128 or 64, causal or not, no window or ALiBi) on
+// v_mfma_f32_32x32x2_f32: exact f32 products, f32 sums, softmax in f32 against a
+// running maximum (the reference's stableSoftmaxRow takes the row max, exp in
+// float64 and a sequential f32 sum; the order of the sums differs, the f32 bar
+// holds).  One 256-thread block per (128-query tile, head, batch), wave w owning 32
+// queries; K/V stream through LDS in 32-key tiles (16 KB each at D = 128), double
+// buffered, copied HBM -> LDS by buffer_load ... lds; two blocks per CU.
+//   S^T[key, q] = K . Q^T: MFMA step s of 4-step group g gives half h = lane / 32 of
+//     the wave d = 8 g + 4 h + s, so a lane's K operands for a group are one 16-byte
+//     LDS read of its key row (chunk c of row r at c ^ (r % 16): the 16 rows an LDS
+//     cycle serves on distinct banks) and Q^T sits in registers for the whole loop.
+//   The accumulator's register r = 4 g + s of lane (q, h) holds key 8 g + 4 h + s, so
+//     P^T is already the B operand of O^T[d, q] += V^T . P^T for the same k order;
+//     V^T's operand is one float per lane and step from the row-major V tile (row k
+//     keeps column d at d ^ 32 (k / 4 % 2), so the two half-waves, rows k and k + 4,
+//     read opposite halves of the bank line).
+template <int D> struct PfF32Dim {
+    static_assert(D == 128 || D == 64, "head dim 128 or 64");
+    static constexpr int BN = 32;               // keys per tile
+    static constexpr int RB = D * 4;            // row bytes
+    static constexpr int NC = RB / 16;          // 16-byte chunks per row
+    static constexpr int TILE = BN * RB;        // 16 or 8 KB
+    static constexpr int KG = D / 8;            // 4-step groups over d
+    static constexpr int DB = D / 32;           // O^T blocks of 32 dims
+    static constexpr int RPI = 64 / NC;         // rows per copy instruction
+    static constexpr int NI = BN / RPI / 4;     // copy instructions per wave and tensor
+    static constexpr int kswz(int r) { return r & 15; }
+    static constexpr int vswz(int r) { return ((r >> 2) & 1) << 3; }   // in chunks (8 = 32 floats)
+};
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
+    using T = PfF32Dim<D>;
+    constexpr int BM = fa::BM, BN = T::BN;
+    __shared__ __attribute__((aligned(1024))) char k0s[T::TILE];
+    __shared__ __attribute__((aligned(1024))) char k1s[T::TILE];
+    __shared__ __attribute__((aligned(1024))) char v0s[T::TILE];
+    __shared__ __attribute__((aligned(1024))) char v1s[T::TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+
+    // block -> (query tile, batch, head), heaviest tiles first, a kv group's query
+    // heads on one XCD (as prefill_kernel)
+    const int id = blockIdx.x;
+    const int bh = a.batch * a.heads;
+    const int qt = a.causal ? (a.qtiles - 1 - id / bh) : (id / bh);
+    int b, hd;
+    if (a.xcd_map) {
+        const int G = a.heads / a.kv_heads;
+        const int j = id % bh;
+        const int xcd = j & 7, slot = j >> 3;
+        const int grp = (slot / G) * 8 + xcd;
+        b = grp / a.kv_heads;
+        hd = (grp % a.kv_heads) * G + slot % G;
+    } else {
+        b = (id % bh) / a.heads;
+        hd = id % a.heads;
+    }
+    const int kvh = hd / (a.heads / a.kv_heads);
+    const int q0 = qt * BM;
+    const float *const qp = reinterpret_cast<const float *>(a.q);
+    const float *const kp = reinterpret_cast<const float *>(a.k);
+    const float *const vp = reinterpret_cast<const float *>(a.v);
+    const int64_t qrs = (int64_t)a.heads * D, krs = (int64_t)a.kv_heads * D;
+    const float *qbase = qp + (int64_t)b * a.seq_q * qrs + (int64_t)hd * D;
+    const float *kbase = kp + (int64_t)b * a.seq_k * krs + (int64_t)kvh * D;
+    const float *vbase = vp + (int64_t)b * a.seq_k * krs + (int64_t)kvh * D;
+
+    // this lane's query and its Q^T operands: qf[g] = Q[qi][8 g + 4 h .. + 3]
+    const int qfirst = q0 + 32 * wave;
+    const int qlast = min(qfirst + 31, a.seq_q - 1);
+    const int qi = qfirst + l32;
+    f32x4 qf[T::KG];
+    {
+        const int qload = min(qi, a.seq_q - 1);   // rows past the end compute garbage, never stored
+#pragma unroll
+        for (int g = 0; g < T::KG; ++g)
+            qf[g] = *reinterpret_cast<const f32x4 *>(qbase + (int64_t)qload * qrs + 8 * g + 4 * h);
+    }
+
+    int kend = a.seq_k;
+    if (a.causal) kend = min(kend, min(q0 + BM, a.seq_q) + a.shift);
+    const int ntiles = kend > 0 ? (kend + BN - 1) / BN : 0;
+    int nfree = a.seq_k / BN;
+    if (a.causal) nfree = min(nfree, q0 + a.shift + 1 > 0 ? (q0 + a.shift + 1) / BN : 0);
+    nfree = min(nfree, ntiles);
+
+    // copy offsets (source side, swizzled): wave w fills rows 4 RPI i + RPI w + lane / NC
+    int kg[4], vg[4];
+    {
+        const int rs4 = a.kv_heads * D * 4;
+        const int pos = lane % T::NC;
+#pragma unroll
+        for (int i = 0; i < T::NI; ++i) {
+            const int row = 4 * T::RPI * i + T::RPI * wave + lane / T::NC;
+            kg[i] = row * rs4 + ((pos ^ T::kswz(row)) << 4);
+            vg[i] = row * rs4 + ((pos ^ T::vswz(row)) << 4);
+        }
+    }
+    auto copy_tile = [&](int kv0, char *kdst, char *vdst) __attribute__((always_inline)) {
+        const int rs4 = a.kv_heads * D * 4;
+        const int rows = min(a.seq_k - kv0, BN);
+        const int bytes = (rows - 1) * rs4 + D * 4;
+        const int64_t base = (int64_t)kv0 * a.kv_heads * D;
+        const __amdgpu_buffer_rsrc_t kd =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(kbase + base), (short)0, bytes, fa::BUF_WORD3);
+        const __amdgpu_buffer_rsrc_t vd =
+            __builtin_amdgcn_make_buffer_rsrc((void *)(vbase + base), (short)0, bytes, fa::BUF_WORD3);
+        // (constant trip counts with a guard: a loop bound that depends on the template
+        // arguments inside a lambda loses the kernel's host stub)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < T::NI)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(kd, (lds_void *)(kdst + (4 * T::RPI * i + T::RPI * wave) * T::RB),
+                                                         16, kg[i], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < T::NI)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vd, (lds_void *)(vdst + (4 * T::RPI * i + T::RPI * wave) * T::RB),
+                                                         16, vg[i], 0, 0, 0);
+    };
+    // fragment reads: K row l32, group g at chunk (2 g + h) ^ kswz(l32); V row
+    // 8 g + 4 h + s, column (32 db + l32) ^ 32 h (vswz(row) = 8 chunks iff h = 1)
+    const int kr = l32 * T::RB;
+    int vr[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) vr[db] = 4 * h * T::RB + (((32 * db + l32) ^ (32 * h)) << 2);
+
+    f32x16 o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = (f32x16){};
+    float m = -INFINITY, l = 0.0f;
+    const float c = a.scale_log2;
+
+    auto step = [&](const char *ks, const char *vs, int kv0, bool masked) __attribute__((always_inline)) {
+        f32x16 sacc = (f32x16){};
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            if (g >= T::KG) break;
+            const f32x4 kv = *reinterpret_cast<const f32x4 *>(ks + kr + (((2 * g + h) ^ T::kswz(l32)) << 4));
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[s4], qf[g][s4], sacc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);   // one group's K read live at a time
+        }
+        // register r: key kv0 + 8 (r / 4) + 4 h + r % 4, query qi
+        if (masked) {
+            const int last = a.causal ? min(qi + a.shift, a.seq_k - 1) : a.seq_k - 1;
+            const int lim = last - kv0 - 4 * h;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (8 * (r >> 2) + (r & 3) > lim) sacc[r] = -INFINITY;
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[r]);
+        tmax = swap_halves_max(tmax) * c;
+        if (__any(tmax > m)) {   // a new maximum: rescale O and l (wave-uniform branch)
+            const float mnew = fmaxf(m, tmax);
+            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mnew);
+            m = mnew;
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                if (db >= T::DB) break;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+            }
+        }
+        const float mref = m == -INFINITY ? 0.0f : m;
+        float psum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sacc[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c, -mref));
+            psum += sacc[r];
+        }
+        l += psum;
+        // O^T += V^T . P^T, step (g, s4): V row 8 g + 4 h + s4, P^T register 4 g + s4; a
+        // scheduling barrier per group keeps one group's V reads live at a time
+#pragma unroll
+        for (int g = 0; g < BN / 8; ++g) {
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    if (db >= T::DB) break;
+                    const float vv = *reinterpret_cast<const float *>(vs + (8 * g + s4) * T::RB + vr[db]);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, sacc[4 * g + s4], o[db], 0, 0, 0);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    if (0 < ntiles) copy_tile(0, k0s, v0s);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    auto tile = [&](int it, const char *kc, const char *vc, char *kn, char *vn) __attribute__((always_inline)) {
+        const int kv0 = it * BN;
+        if (it + 1 < ntiles) copy_tile(kv0 + BN, kn, vn);
+        if (it < nfree) step(kc, vc, kv0, false);
+        else if (!a.causal || kv0 <= qlast + a.shift) step(kc, vc, kv0, true);   // waves whose queries all precede it skip it
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    };
+    int it = 0;
+    for (; it + 1 < ntiles; it += 2) {
+        tile(it, k0s, v0s, k1s, v1s);
+        tile(it + 1, k1s, v1s, k0s, v0s);
+    }
+    if (it < ntiles) tile(it, k0s, v0s, k1s, v1s);
+
+    // normalise and store: lane holds O[qi][32 db + 8 (r/4) + 4 h + r%4]
+    const float ltot = swap_halves_sum(l);
+    const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+    if (qi < a.seq_q) {
+        float *orow = reinterpret_cast<float *>(a.o) + (int64_t)b * a.seq_q * qrs + (int64_t)qi * qrs + (int64_t)hd * D;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            if (db >= T::DB) break;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                f32x4 v;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = o[db][4 * rb + i] * inv;
+                *reinterpret_cast<f32x4 *>(orow + 32 * db + 8 * rb + 4 * h) = v;
+            }
+        }
+    }
+}
+
+// f32 MultiHeadAttention on prefill_f32_kernel: head dim 128 or 64, at least 16 query
+// rows, no sliding window or ALiBi (those keep the general kernel).
+static bool launch_prefill_f32(const MhaArgs &m, hipStream_t s, int *status) {
+    if (m.dim != 128 && m.dim != 64) return false;
+    if (m.seq_q < 16 || m.alibi != 0.0f || (m.window > 0 && m.window < m.seq_q)) return false;
+    if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF) return false;
+    if (m.kv_heads > 32768) return false;   // a 32-row K/V tile spans < 2^31 bytes
+    const uintptr_t mask = 15;
+    if ((reinterpret_cast<uintptr_t>(m.q) | reinterpret_cast<uintptr_t>(m.k) |
+         reinterpret_cast<uintptr_t>(m.v) | reinterpret_cast<uintptr_t>(m.o)) & mask)
+        return false;
+    PrefillArgs a;
+    a.q = static_cast<const uint16_t *>(m.q);
+    a.k = static_cast<const uint16_t *>(m.k);
+    a.v = static_cast<const uint16_t *>(m.v);
+    a.o = static_cast<uint16_t *>(m.o);
+    a.batch = (int)m.batch;
+    a.seq_q = (int)m.seq_q;
+    a.seq_k = (int)m.seq_k;
+    a.heads = (int)m.heads;
+    a.kv_heads = (int)m.kv_heads;
+    a.qtiles = (int)((m.seq_q + fa::BM - 1) / fa::BM);
+    a.causal = m.causal;
+    a.shift = (int)m.shift;
+    a.window = 0;
+    a.alibi_s = 0.0f;
+    a.xcd_map = ((a.batch * a.kv_heads) % 8 == 0) ? 1 : 0;
+    a.scale_log2 = m.scale * 1.4426950408889634f;
+    const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;
+    if (blocks > 0x7FFFFFFF) return false;
+    if (m.dim == 128) prefill_f32_kernel<128><<<(unsigned)blocks, 256, 0, s>>>(a);
+    else prefill_f32_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(a);
+    *status = check_launch("prefill f32 mfma");
+    return true;
+}
+
 bool launch_prefill_mfma(const MhaArgs &m, int dtype, hipStream_t s, int *status) {
+    if (dtype == PUTER_F32) return launch_prefill_f32(m, s, status);
     if ((dtype != PUTER_BF16 && dtype != PUTER_F16) || (m.dim != 128 && m.dim != 64)) return false;
     if (m.dim == 64 && m.seq_q == 1) return false;   // one query row: the general kernel (no 127 padding rows)
     if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF)
