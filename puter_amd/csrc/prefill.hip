@@ -1,5 +1,6 @@
 // MFMA flash-attention prefill: bf16 or f16 Q/K/V (prefill_kernel<dtype, head
-// dim, window>), f32 accumulation, output in the input format, head_dim 128 or 64, GQA,
+// dim, window>; f32 Q/K/V on prefill_f32_kernel, described where it is defined),
+// f32 accumulation, output in the input format, head_dim 128 or 64, GQA,
 // optional causal mask: key k is visible to query q when
 // k <= q + shift.  MultiHeadAttention passes shift = seqK - seqQ (bottom-right
 // aligned, device/cpu/attention/typed_compute.go:166-168);
