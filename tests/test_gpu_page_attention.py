@@ -281,8 +281,9 @@ def test_page_write_prefill_sized_duplicates_far_apart(backend, dt, inner, rows)
     (5, 300, 4, 1, 128, True),       # bottom-right aligned causal
     (64, 64, 8, 2, 128, False),
     (1, 513, 8, 2, 128, True),       # decode shape
-    (300, 300, 4, 2, 128, True),     # ragged query and key tiles (f32: the f32 MFMA prefill kernel)
-    (200, 520, 8, 4, 64, True),      # causal shift 320, head dim 64
+    (300, 300, 8, 2, 128, True),     # ragged query and key tiles (f32: the f32 MFMA prefill kernel, 24 blocks)
+    (200, 520, 16, 4, 64, True),     # causal shift 320, head dim 64 (32 blocks)
+    (150, 150, 16, 4, 128, False),   # not causal, ragged tiles (32 blocks)
 ])
 def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
     import puter_amd
