@@ -18,6 +18,8 @@ void set_error(const char *fmt, ...);
 int fail(int status, const char *fmt, ...);
 int check_launch(const char *what);
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+// compute units of the current device, cached per device (256 when the query fails)
+int device_cus();
 
 // The library's scratch buffer on the current device (split-K partials of Matmul
 // and of one-row attention), held for one call's launches: the constructor orders

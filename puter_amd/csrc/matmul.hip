@@ -1104,7 +1104,7 @@ static int launch_skinny(void *out, const void *left, const void *right, int64_t
 }
 
 // Compute units of the current device, cached per device (256 on MI355X).
-static int device_cus() {
+int device_cus() {
     static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

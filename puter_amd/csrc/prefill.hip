@@ -136,6 +136,12 @@ struct PrefillArgs {
     int window;        // > 0: key k visible to query q only if k > q - window
     float alibi_s;     // ALiBi slope / scale: the dot gains alibi_s * (k - q) before scaling
     float scale_log2;  // softmax scale * log2(e)
+    // f32 kernel, key range split over blockIdx.y (split_tiles key tiles each): per
+    // split, query row and head the (max, sum) and the unnormalised output row, in
+    // [split][batch][query][head] order; null when unsplit
+    int split_tiles = 0;
+    float2 *part_ml = nullptr;
+    float *part_o = nullptr;
 };
 
 template <int D> struct PrefillState {
@@ -838,26 +844,52 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
         }
     };
 
-    if (0 < ntiles) copy_tile(0, k0s, v0s);
+    // this block's key tiles: all, or split blockIdx.y's run of split_tiles
+    int tlo = 0, thi = ntiles;
+    if (a.split_tiles > 0) {
+        tlo = min(ntiles, (int)blockIdx.y * a.split_tiles);
+        thi = min(ntiles, tlo + a.split_tiles);
+    }
+    if (tlo < thi) copy_tile(tlo * BN, k0s, v0s);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     auto tile = [&](int it, const char *kc, const char *vc, char *kn, char *vn) __attribute__((always_inline)) {
         const int kv0 = it * BN;
-        if (it + 1 < ntiles) copy_tile(kv0 + BN, kn, vn);
+        if (it + 1 < thi) copy_tile(kv0 + BN, kn, vn);
         if (it < nfree) step(kc, vc, kv0, false);
         else if (!a.causal || kv0 <= qlast + a.shift) step(kc, vc, kv0, true);   // waves whose queries all precede it skip it
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
     };
-    int it = 0;
-    for (; it + 1 < ntiles; it += 2) {
+    int it = tlo;
+    for (; it + 1 < thi; it += 2) {
         tile(it, k0s, v0s, k1s, v1s);
         tile(it + 1, k1s, v1s, k0s, v0s);
     }
-    if (it < ntiles) tile(it, k0s, v0s, k1s, v1s);
+    if (it < thi) tile(it, k0s, v0s, k1s, v1s);
 
-    // normalise and store: lane holds O[qi][32 db + 8 (r/4) + 4 h + r%4]
     const float ltot = swap_halves_sum(l);
+    if (a.part_ml) {
+        // split: the row's (max, sum) and unnormalised output to the partials
+        if (qi < a.seq_q) {
+            const int64_t prow = (((int64_t)blockIdx.y * a.batch + b) * a.seq_q + qi) * a.heads + hd;
+            if (h == 0) a.part_ml[prow] = make_float2(m, ltot);
+            float *orow = a.part_o + prow * D;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                if (db >= T::DB) break;
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    f32x4 v;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = o[db][4 * rb + i];
+                    *reinterpret_cast<f32x4 *>(orow + 32 * db + 8 * rb + 4 * h) = v;
+                }
+            }
+        }
+        return;
+    }
+    // normalise and store: lane holds O[qi][32 db + 8 (r/4) + 4 h + r%4]
     const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
     if (qi < a.seq_q) {
         float *orow = reinterpret_cast<float *>(a.o) + (int64_t)b * a.seq_q * qrs + (int64_t)qi * qrs + (int64_t)hd * D;
@@ -873,6 +905,35 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
             }
         }
     }
+}
+
+// Merges the key splits of prefill_f32_kernel: one wave per (batch, query, head) row,
+// lanes over the head dims; the splits are folded in order with weights
+// exp2(m_s - M) (m in the scaled log2 domain), O = sum w_s O_s / sum w_s l_s; a row
+// with no visible key (every m = -inf) is 0, as in the unsplit kernel.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_f32_combine_kernel(PrefillArgs a, int splits, int64_t rows) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    float M = -INFINITY;
+    for (int s = 0; s < splits; ++s) M = fmaxf(M, a.part_ml[s * rows + row].x);
+    float acc[D / 64] = {}, lsum = 0.0f;
+    if (M != -INFINITY) {
+        for (int s = 0; s < splits; ++s) {
+            const float2 ml = a.part_ml[s * rows + row];
+            const float w = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
+            lsum += w * ml.y;
+            const float *po = a.part_o + (s * rows + row) * D;
+#pragma unroll
+            for (int j = 0; j < D / 64; ++j) acc[j] += w * po[64 * j + lane];
+        }
+    }
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    // row = (batch, query, head): the output row of the same index, D floats
+    float *out = reinterpret_cast<float *>(a.o) + row * D;
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) out[64 * j + lane] = acc[j] * inv;
 }
 
 // f32 MultiHeadAttention on prefill_f32_kernel: head dim 128 or 64, at least 16 query
@@ -909,6 +970,52 @@ static bool launch_prefill_f32(const MhaArgs &m, hipStream_t s, int *status) {
     // 256 x 8 x 128 (16) 35.3 against 43.4; from 24 blocks this kernel wins (384 x 8 x
     // 64: 32.9 against 36.0, 4 x 128 x 8 x 64: 15.0 against 24.5)
     if (blocks < 24 || blocks > 0x7FFFFFFF) return false;
+    // small grids split each block's key range over blockIdx.y, partials in the
+    // library's scratch: the longest block's key loop, the critical path, shrinks with
+    // the split count.  Causal grids of under two blocks per CU aim at four blocks per
+    // CU in runs of at least 8 key tiles (the triangle leaves most CUs idle while the
+    // last query tiles run: B1 S4096 8 x 64 causal 296 -> 221 us, S2048 8 x 128 154 ->
+    // 146 us), other grids of under one block per CU at two, in runs of at least 16
+    // (B1 S2048 8 x 64, 150 -> 88 us; more splits lose there).  A stream that is
+    // capturing a graph keeps the unsplit kernel (the scratch cannot grow there)
+    const int64_t cus = device_cus();
+    const int64_t ktiles = (m.seq_k + 31) / 32;
+    int64_t splits = 1;
+    if (a.causal && blocks < 2 * cus)
+        splits = std::max<int64_t>(1, std::min<int64_t>((4 * cus + blocks - 1) / blocks, ktiles / 8));
+    else if (!a.causal && blocks < cus)
+        splits = std::max<int64_t>(1, std::min<int64_t>((2 * cus + blocks - 1) / blocks, ktiles / 16));
+    if (splits > 1) {
+        hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cst) != hipSuccess || cst != hipStreamCaptureStatusNone) splits = 1;
+    }
+    if (splits > 1) {
+        a.split_tiles = (int)((ktiles + splits - 1) / splits);
+        splits = (ktiles + a.split_tiles - 1) / a.split_tiles;
+        const int64_t rows = m.batch * m.seq_q * m.heads;
+        const size_t need = (size_t)(splits * rows) * (sizeof(float2) + (size_t)m.dim * sizeof(float));
+        ScratchLease lease(need, s);
+        if (lease.status()) {
+            *status = lease.status();
+            return true;
+        }
+        // outputs first: splits * rows * D floats keep the (max, sum) pairs 16-byte aligned
+        a.part_o = static_cast<float *>(lease.ptr());
+        a.part_ml = reinterpret_cast<float2 *>(a.part_o + splits * rows * m.dim);
+        const dim3 grid((unsigned)blocks, (unsigned)splits);
+        const unsigned cblocks = (unsigned)((rows + 3) / 4);
+        if (m.dim == 128) {
+            prefill_f32_kernel<128><<<grid, 256, 0, s>>>(a);
+            prefill_f32_combine_kernel<128><<<cblocks, 256, 0, s>>>(a, (int)splits, rows);
+        } else {
+            prefill_f32_kernel<64><<<grid, 256, 0, s>>>(a);
+            prefill_f32_combine_kernel<64><<<cblocks, 256, 0, s>>>(a, (int)splits, rows);
+        }
+        const int rc = check_launch("prefill f32 mfma split");
+        const int fin = lease.finish();
+        *status = rc ? rc : fin;
+        return true;
+    }
     if (m.dim == 128) prefill_f32_kernel<128><<<(unsigned)blocks, 256, 0, s>>>(a);
     else prefill_f32_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(a);
     *status = check_launch("prefill f32 mfma");

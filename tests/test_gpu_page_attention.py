@@ -299,6 +299,26 @@ def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
                  elem_tol=1e-3 if dt == O.F32 else None, what="mha")
 
 
+@pytest.mark.parametrize("sq,sk,h,kvh,d,causal", [
+    (1024, 1024, 4, 1, 64, True),    # 32 blocks, 4 runs of 8 key tiles; the first query tile's last 3 are empty
+    (200, 2100, 12, 4, 64, False),   # 24 blocks, 4 runs of 17 tiles, the last ragged
+    (300, 1300, 8, 2, 128, True),    # head dim 128, causal shift 1000, 5 runs of 9 tiles, the last ragged
+])
+def test_mha_f32_key_split(backend, sq, sk, h, kvh, d, causal):
+    """f32 grids under one block per CU split each block's key range over blockIdx.y
+    and merge the runs' (max, sum, output) partials in a second kernel."""
+    import puter_amd
+    dt = O.F32
+    q = encode(seeded(190 + sq, (sq, h * d)), dt)
+    k = encode(seeded(191 + sk, (sk, kvh * d)), dt)
+    v = encode(seeded(192 + sk, (sk, kvh * d)), dt)
+    ref = decode(O.mha(q, k, v, h, d, causal=causal, kv_heads=kvh, dtype=dt), dt)
+    out = empty_dev((sq, h * d), NP[dt])
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, 0, 0.0, kvh)
+    backend.MultiHeadAttention(cfg, to_dev(q), to_dev(k), to_dev(v), out, sq, sk, dt)
+    assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], elem_tol=1e-3, what="mha split")
+
+
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("b,sk,h,kvh,causal,window", [
     (1, 4096, 32, 8, True, 0),     # configs[4]'s heads at one sequence's full context
