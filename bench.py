@@ -804,7 +804,8 @@ def profile_workload(torch, be, puter, spec, launches):
     NAME --profile-launches N`): `norm:ROWSxHIDDEN` (fused GatedResidual+RMSNorm
     bf16 on one shape, each launch on the next window of 1 GiB pools so none is
     served from the 256 MB last-level cache, then one 1 GiB calibration copy),
-    `stream` (the 2-read/2-write stream probe in its three launch shapes),
+    `stream` (the 2-read/2-write stream probe in its three launch shapes), `mfma`
+    (the MFMA rate probe, alone and in the prefill's dataflow),
     `prefill` (configs[3]), `decode_bf16` / `decode_fp8` (configs[4]), `pages`
     (the page write / gather legs at configs[4]'s pool).  Each launch is preceded
     by nothing else on the stream."""
@@ -835,6 +836,33 @@ def profile_workload(torch, be, puter, spec, launches):
                 rc = be.lib.puter_hip_stream_probe(*(C.c_void_p(b.data_ptr()) for b in bufs), vectors, shape,
                                                    C.c_void_p(stream))
                 assert rc == 0, rc
+    elif spec == "mfma":
+        # the matrix cores' rate on random bf16 operands (puter_hip_mfma_probe): mode 0
+        # the MFMAs alone, mode 1 the prefill's 64-key tile dataflow with no memory
+        # traffic; 2048 blocks held at two per CU, `launches` timed launches each
+        import ctypes as C
+        gen = torch.Generator(device="cuda").manual_seed(0x5EED0004)
+        ops = torch.randn(8192, device="cuda", dtype=torch.bfloat16, generator=gen)
+        blocks, iters = 2048, 256
+        out = torch.empty(blocks * 256, device="cuda", dtype=torch.float32)
+        stream = torch.cuda.current_stream().cuda_stream
+        flops = blocks * 4 * iters * 32 * 32768.0
+        for mode in (0, 1):
+            def launch():
+                rc = be.lib.puter_hip_mfma_probe(C.c_void_p(ops.data_ptr()), C.c_void_p(out.data_ptr()), blocks,
+                                                 iters, mode, C.c_void_p(stream))
+                assert rc == 0, rc
+            launch()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(launches):
+                launch()
+            e1.record()
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / launches
+            log(f"mfma probe mode {mode}: {ms * 1e3:.1f} us per launch, {flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s "
+                f"({flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS:.3f} of the dense bf16 peak)")
     elif spec == "prefill":
         fn = prefill(torch, be, puter, return_fn=True)
         for _ in range(launches):

@@ -404,6 +404,17 @@ PUTER_API int puter_hip_matmul_noalloc(void *out, const void *left, const void *
 PUTER_API int puter_hip_stream_probe(const void *a, const void *b, void *c, void *d, int64_t vectors,
                                      int shape, void *stream);
 
+/* Diagnostic (no counterpart in the reference): MFMA rate probe.  blocks     */
+/* 256-thread blocks (two per CU), each wave running iters iterations of 32   */
+/* v_mfma_f32_32x32x16_bf16 on operands read once from operands (16 KiB of    */
+/* bf16, 16-byte aligned): mode 0 the MFMAs alone on 4 accumulator chains;    */
+/* mode 1 the prefill's 64-key tile dataflow (S = K.Q^T, exp2 softmax with    */
+/* the row sum and bf16 narrowing, O += V^T.P^T) with no memory traffic.      */
+/* out receives blocks * 256 floats.  Flops per launch: blocks * 4 * iters *  */
+/* 32 * 32768.                                                                */
+PUTER_API int puter_hip_mfma_probe(const void *operands, void *out, int64_t blocks, int iters, int mode,
+                                   void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -94,6 +94,7 @@ SIGNATURES = {
     "puter_hip_quant": ([vp, vp, i64, C.c_float, i32, i32, i32, vp], i32),
     "puter_hip_matmul": ([vp, vp, vp, i64, i64, i64, i32, vp], i32),
     "puter_hip_stream_probe": ([vp, vp, vp, vp, i64, i32, vp], i32),
+    "puter_hip_mfma_probe": ([vp, vp, i64, i32, i32, vp], i32),
     "puter_hip_matmul_noalloc": ([vp, vp, vp, i64, i64, i64, i32, vp], i32),
 }
 

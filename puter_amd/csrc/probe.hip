@@ -10,6 +10,8 @@
 //            between the two stores, as the wave-per-row norm kernel does.
 // c = a + b (as u32 lanes) is stored before the sum, d = (a ^ b) + (sum & 1)
 // after it, so neither store can be dropped.
+// The MFMA rate probe further down measures the matrix cores' rate on random
+// operands, alone and in the prefill kernel's dataflow without memory traffic.
 #include "common.hpp"
 
 namespace puter {
@@ -67,9 +69,108 @@ __global__ __launch_bounds__(256) void probe_wave_row(const pu32x4 *a, const pu3
     for (int j = 0; j < 16; ++j) pst((x[j] ^ y[j]) + (__float_as_uint(s) & 1u), d + off + j * 64 + lane);
 }
 
+// MFMA rate probe (diagnostic): 256-thread blocks held at two per CU (2 waves per
+// SIMD, as the prefill kernel runs) by 64 KiB of dynamic LDS that is never touched.
+// Operands come from a 16 KiB buffer of random bf16 read once into registers (the
+// matrix cores draw more power, and the part clocks lower, on random data than on
+// constants); each lane's 8 Q^T and 8 K fragments are 16 bytes at (i * 64 + lane).
+//   mode 0: 32 v_mfma_f32_32x32x16_bf16 per iteration on 4 accumulator chains;
+//   mode 1: the prefill's per-tile dataflow for 32 queries x 64 keys x 128 dims with
+//           no memory traffic: S^T = K . Q^T (16 MFMAs into two chunks), p =
+//           exp2(s c - m) with the row sum and the narrowing to bf16, O^T += V^T .
+//           P^T (16 MFMAs; V^T fragments reuse the K registers).
+// Each wave stores one float per lane so that nothing is dropped.
+typedef __bf16 pbf16x8 __attribute__((ext_vector_type(8)));
+typedef float pf32x16 __attribute__((ext_vector_type(16)));
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void probe_mfma(const pbf16x8 *ops, float *out, int iters) {
+    const int lane = threadIdx.x & 63;
+    pbf16x8 qf[8], kf[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        qf[i] = ops[i * 64 + lane];
+        kf[i] = ops[512 + i * 64 + lane];
+    }
+    float res = 0.0f;
+    if constexpr (MODE == 0) {
+        pf32x16 acc[4] = {};
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t], qf[(t + c) & 7], acc[c], 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) res += acc[c][r];
+    } else {
+        pf32x16 o[4] = {};
+        float l = 0.0f;
+        const float sc = 0.1275f;   // 1/sqrt(128) * log2(e)
+        for (int it = 0; it < iters; ++it) {
+            pf32x16 s[2] = {};
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    s[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[(t + c) & 7], qf[t], s[c], 0, 0, 0);
+            pbf16x8 pf[2][2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][8 * h + j], sc, -1.0f));
+                        l += p;
+                        pf[c][h][j] = (__bf16)p;
+                    }
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+                        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[(4 * c + 2 * h + d) & 7], pf[c][h], o[d], 0, 0, 0);
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) res += o[d][r];
+        res += l;
+    }
+    out[(int64_t)blockIdx.x * 256 + threadIdx.x] = res;
+}
+
 }  // namespace puter
 
 using namespace puter;
+
+extern "C" int puter_hip_mfma_probe(const void *operands, void *out, int64_t blocks, int iters, int mode,
+                                    void *stream) {
+    if (blocks < 0 || blocks > 0x7FFFFFFF || iters < 0 || mode < 0 || mode > 1)
+        return fail(PUTER_ERR_INVALID, "mfma probe: invalid arguments");
+    if (blocks == 0) return PUTER_OK;
+    if (!operands || !out) return fail(PUTER_ERR_NIL, "mfma probe: nil buffer");
+    if (!aligned16(operands) || !aligned16(out)) return fail(PUTER_ERR_INVALID, "mfma probe: buffers must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const pbf16x8 *ops = static_cast<const pbf16x8 *>(operands);
+    float *o = static_cast<float *>(out);
+    constexpr size_t pin = 64 * 1024;   // two blocks per CU
+    if (mode == 0) {
+        if (hipFuncSetAttribute((const void *)probe_mfma<0>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pin) != hipSuccess)
+            return fail(PUTER_ERR_LAUNCH, "mfma probe: cannot set the LDS size");
+        probe_mfma<0><<<(unsigned)blocks, 256, pin, s>>>(ops, o, iters);
+    } else {
+        if (hipFuncSetAttribute((const void *)probe_mfma<1>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pin) != hipSuccess)
+            return fail(PUTER_ERR_LAUNCH, "mfma probe: cannot set the LDS size");
+        probe_mfma<1><<<(unsigned)blocks, 256, pin, s>>>(ops, o, iters);
+    }
+    return check_launch("mfma probe");
+}
 
 extern "C" int puter_hip_stream_probe(const void *a, const void *b, void *c, void *d, int64_t vectors, int shape,
                                       void *stream) {

@@ -93,6 +93,10 @@ def test_cast_activation_page_validation(lib):
     assert lib.puter_hip_stream_probe(FAKE, FAKE, FAKE, FAKE, 1024, 3, None) == _lib.ERR_INVALID
     assert lib.puter_hip_stream_probe(FAKE, FAKE, FAKE, FAKE, 1000, 1, None) == _lib.ERR_INVALID
     assert lib.puter_hip_stream_probe(None, None, None, None, 0, 0, None) == _lib.OK
+    # MFMA probe: modes 0-1, non-negative sizes; no blocks is a no-op
+    assert lib.puter_hip_mfma_probe(FAKE, FAKE, 8, 4, 2, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_mfma_probe(FAKE, FAKE, -1, 4, 0, None) == _lib.ERR_INVALID
+    assert lib.puter_hip_mfma_probe(None, None, 0, 4, 0, None) == _lib.OK
     # RoPEPairs is F32 only (device/cpu/rope/ops.go:10-14); zero pairs is a no-op
     assert lib.puter_hip_rope_pairs(FAKE, FAKE, FAKE, FAKE, 8, 2, None) == _lib.ERR_INVALID
     assert lib.puter_hip_rope_pairs(None, None, None, None, 0, 0, None) == _lib.OK
