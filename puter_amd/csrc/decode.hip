@@ -113,6 +113,7 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
     // one kv head per XCD: bf16 225.5 -> 220.4 us, fp8 136.4 -> 132.6 us on the
     // 64-sequence decode pool (one process); eight bf16 heads (2 KB) gave 223.7 us.
     int kvh, split, b;
+    int64_t chunk;
     {
         int gk = W16 ? 4 : 8;
         while (gk > 1 && a.kv_heads % gk) gk >>= 1;
@@ -128,14 +129,50 @@ __global__ __launch_bounds__(256, 2) void decode_block_kernel(DecodeArgs a) {
             cg = (C / 8) * 8 + (L - full) / gk;
         }
         kvh = (int)((cg % NG) * gk + kvl);
-        const int64_t chunk = cg / NG;
+        chunk = cg / NG;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    int ctx;
+    if (a.ctx && a.batch <= 256 && !W16) {
+        // fp8 pools, live chunks first: chunk c is the c-th live (sequence, split) pair,
+        // sequences in order, so the blocks past the last live pair, which exit at once,
+        // are dispatched after all the work instead of among it (every wave of the block
+        // finds the same pair: a prefix sum of the sequences' split counts, 64 at a
+        // time).  On the 64-sequence decode pool, interleaved in one process, bit-
+        // identical: fp8 133.9 -> 131.4 us; the 16-bit kernel lost 1.4% with it (212.4
+        // -> 215.3 us) and keeps the plain order
+        b = -1;
+        split = 0;
+        ctx = 0;
+        int64_t base = 0;
+        for (int j0 = 0; j0 < a.batch; j0 += 64) {   // wave-uniform
+            const int j = j0 + lane;
+            const int cx = j < a.batch ? (int)min((int64_t)a.ctx[j], a.max_context) : 0;
+            const int ns = cx > 0 ? (cx + kSplit - 1) / kSplit : 0;
+            int incl = ns;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            const int total = __shfl(incl, 63, 64);
+            if (chunk < base + total) {
+                const int lj = __builtin_ctzll(__ballot(base + incl > chunk));
+                b = j0 + lj;
+                split = __builtin_amdgcn_readfirstlane((int)(chunk - base - (__shfl(incl, lj, 64) - __shfl(ns, lj, 64))));
+                ctx = __builtin_amdgcn_readfirstlane(__shfl(cx, lj, 64));
+                break;
+            }
+            base += total;
+        }
+        if (b < 0) return;   // the whole block: past the last live pair
+    } else {
         split = (int)(chunk % gridDim.y);
         b = (int)(chunk / gridDim.y);
+        ctx = a.ctx ? (int)min((int64_t)a.ctx[b], a.max_context) : (int)a.max_context;
     }
-    const int ctx = a.ctx ? (int)min((int64_t)a.ctx[b], a.max_context) : (int)a.max_context;
     const int t0 = split * kSplit;
     if (t0 >= ctx) return;   // the whole block
-    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tw0 = t0 + TW * wave;
     const int64_t inner = a.kv_heads * D;

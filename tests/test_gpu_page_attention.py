@@ -744,6 +744,29 @@ def test_paged_decode_bad_page_ids_are_masked(backend, kv_dt):
                  elem_tol=None, what="paged decode, bad page ids")
 
 
+@pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
+@pytest.mark.parametrize("batch,lo,hi", [(70, 1, 600), (300, 1, 40)])
+def test_paged_decode_empty_sequences_and_batches(backend, kv_dt, batch, lo, hi):
+    """Sequences of zero context among live ones in batches of 70 (fp8 pools number
+    the live (sequence, split) pairs with a prefix sum over 64 sequences at a time:
+    two passes) and 300 (past 256 sequences the plain block order).  A sequence with
+    no key has no reference output (the reference's gather yields no rows and its
+    zero-size attention call returns early); this extension writes zeros for it.  The
+    live sequences match the oracle run on them alone."""
+    h, kvh, d, ps = 8, 2, 128, 16
+    ctx, table, total, q, kp, vp, ks, vs = paged_case(8300 + batch, batch, lo, hi, ps, h, kvh, d, kv_dt)
+    empty = [0, 5, 63, 64, batch - 1]
+    ctx[empty] = 0
+    live = ctx > 0
+    ref = O.paged_decode(q[live], kp, vp, table[live], ctx[live], ps, h, kvh, d, kv_dt, ks, vs)
+    out = run_paged_decode(backend, q, kp, vp, table, ctx, ps, total, h, kvh, d, kv_dt, ks, vs)
+    od = out_dtype(kv_dt)
+    got = O.to_f32(out, od).reshape(batch, h * d)
+    assert not got[~live].any()
+    assert_close(got[live], O.to_f32(ref, od).reshape(-1, h * d), TOL[od], elem_tol=None,
+                 what="paged decode, empty sequences")
+
+
 def test_paged_decode_empty_pool(backend):
     """num_pages = 0: every page id is out of range, every token masked, output 0."""
     h, kvh, d, ps, batch = 8, 2, 128, 16, 2
