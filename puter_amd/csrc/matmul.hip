@@ -1019,8 +1019,9 @@ int ScratchLease::finish() {
 // Its split-K partials live in a file-scope device array (one copy per GPU,
 // held until the process ends) instead of the growable scratch.  The array
 // holds 16 MiB, the most any split-K launch here can need: at most 512 blocks
-// (chunks x tiles) of 64 x 128 f32 partials for the 16-bit formats, of 64 x 64
-// for f32.  Host code never passes the array's name to a kernel (in host code it
+// (chunks x tiles) of 64 x 128 f32 partials for the 16-bit formats and for the
+// f32 VALU kernel's 64 x 64 tiles; the f32 MFMA kernel's chunk count is capped so
+// that its partials (chunks x rows x cols floats) fit it.  Host code never passes the array's name to a kernel (in host code it
 // is a stand-in, not a device address): it passes the address
 // hipGetSymbolAddress returns, looked up once per device on that device's first
 // call.  Every no-alloc call on a GPU shares that GPU's array, so such calls
@@ -1281,6 +1282,9 @@ static int launch_matmul_f32(float *out, const float *left, const float *right, 
         int64_t mchunks = 1;
         if (t128 < cus)
             mchunks = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>((2 * cus + t128 - 1) / t128, 16), K / 256));
+        // the partials of every split fit the allocation-free entry point's 16 MiB
+        // array, for both entry points alike (the same chunks: bit-identical results)
+        mchunks = std::min<int64_t>(mchunks, std::max<int64_t>(1, (int64_t)(noalloc::kScratchBytes / ((size_t)(M * N) * sizeof(float)))));
         const int rc = launch_f32_mfma(out, left, right, M, K, N, mchunks, s, tgt);
         if (rc != 1) return rc;
     }

@@ -34,8 +34,10 @@ def _operands(dt, m, k, n, seed):
     (O.BF16, [(128, 4096, 4096), (16, 1024, 512), (5, 256, 136)]),
     (O.F16, [(64, 2048, 1024), (33, 512, 264)]),
     # f32: K split inside each block (128x512x512, no scratch), then K split
-    # across blocks with partials in the scratch (32x256x128), then a tiny one
-    (O.F32, [(128, 512, 512), (32, 256, 128), (7, 13, 5)]),
+    # across blocks on the f32 MFMA kernel with partials in the scratch (256x4096x512,
+    # 16 chunks: 8 MiB; 1024x8192x1024, chunks capped at 4 to fit the 16 MiB), the
+    # VALU kernel's split (32x256x130: N not a multiple of 4), then a tiny one
+    (O.F32, [(128, 512, 512), (256, 4096, 512), (1024, 8192, 1024), (32, 256, 130), (7, 13, 5)]),
 ])
 def test_noalloc_matmul_matches_matmul(backend, dt, shapes):
     import torch
