@@ -17,20 +17,26 @@
  *   - the caller owns every buffer (workspaces included, see
  *     puter_hip_paged_decode_workspace_bytes).  The one allocation the library
  *     makes itself is a split-K scratch shared by puter_hip_matmul (16-bit
- *     formats with at most 512 rows, F32 outputs of fewer than 256 64x64 tiles,
- *     when K is split across blocks rather than inside them) and
+ *     formats with at most 512 rows or under two rounds of 128x128 tiles, F32
+ *     outputs of fewer 128x128 tiles than the device has CUs, when K is split
+ *     across blocks rather than inside them) and
  *     puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16 / f16 at
- *     head dim 128 without ALiBi, or any row over more than 768 keys): one buffer
- *     per device, allocated on first use and grown on demand (Matmul: at most
- *     ~16 MB; one-row attention: the paged decode workspace size, or
- *     batch x heads x ceil(seq_k / 256) x (head_dim + 2) floats).  A growth is stream-ordered on the calling
+ *     head dim 128 without ALiBi, or any row over more than 768 keys) or in F32
+ *     with at least 16 query rows, head dim 128 or 64, no window or ALiBi, and
+ *     fewer 128-query blocks than two per CU (causal) or one per CU (not
+ *     causal): one buffer per device, allocated on first use and grown on
+ *     demand (Matmul: at most 16 MiB; one-row attention: the paged decode
+ *     workspace size, or batch x heads x ceil(seq_k / 256) x (head_dim + 2)
+ *     floats; F32 attention: key splits x batch x seq_q x heads x (head_dim +
+ *     2) floats, at most about 100 MB).  A growth is stream-ordered on the calling
  *     stream (hipFreeAsync of the old buffer after its last user, then
  *     hipMallocAsync): it never blocks the host.  On a stream that is capturing
  *     a HIP graph these calls allocate, free, wait on and record nothing: they
  *     use the buffer held if it is large enough (the graph keeps its address,
  *     so that buffer is never freed: a later growth keeps it and allocates
  *     beside it) and otherwise return PUTER_ERR_INVALID before launching; make
- *     the same call, or a larger one, outside the capture first.  Replays share
+ *     the same call, or a larger one, outside the capture first (F32 attention
+ *     takes its unsplit kernel under capture and uses no scratch).  Replays share
  *     the buffer with eager scratch-using calls until such a growth, so the
  *     caller orders them (one stream, or its own events).
  *
