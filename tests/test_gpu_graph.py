@@ -277,6 +277,41 @@ def test_one_row_mha_graph_uses_the_held_scratch(backend, dt, b, h, kvh, d, seq_
     replay_and_check(3)
 
 
+def test_f32_prefill_captured_runs_unsplit(backend):
+    """f32 MultiHeadAttention on the f32 MFMA kernel splits the key range of small
+    grids with partials in the library's scratch when called eagerly; under capture
+    it takes the unsplit kernel and touches no scratch.  A capture with no eager
+    call before it succeeds; its replays with new inputs match the oracle to the f32
+    bar, and the eager (split) call on the same inputs agrees with them to the same
+    bar."""
+    import torch
+
+    sq_, sk_, h, kvh, d = 1024, 1024, 4, 1, 64   # 32 blocks: 4 key runs when eager
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, True, 0, 0.0, kvh)
+
+    def inputs(seed):
+        return (seeded(seed, (sq_, h * d)), seeded(seed + 1, (sk_, kvh * d)), seeded(seed + 2, (sk_, kvh * d)))
+
+    q0, k0, v0 = inputs(1300)
+    sq, sk, sv = to_dev(q0), to_dev(k0), to_dev(v0)
+    sout = torch.empty(sq.shape, dtype=sq.dtype, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        backend.MultiHeadAttention(cfg, sq, sk, sv, sout, sq_, sk_, O.F32)
+    for step in range(2):
+        q, k, v = inputs(1310 + 10 * step)
+        sq.copy_(to_dev(q)); sk.copy_(to_dev(k)); sv.copy_(to_dev(v))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = to_host(sout, np.float32)
+        want = O.mha(q, k, v, h, d, causal=True, kv_heads=kvh, dtype=O.F32)
+        assert_close(got, want, TOL[O.F32], elem_tol=1e-3, what=f"captured f32 prefill, replay {step}")
+        eager = torch.empty_like(sout)
+        backend.MultiHeadAttention(cfg, sq, sk, sv, eager, sq_, sk_, O.F32)
+        torch.cuda.synchronize()
+        assert_close(to_host(eager, np.float32), got, TOL[O.F32], elem_tol=1e-3, what="eager split against replay")
+
+
 def test_capture_that_would_grow_the_scratch_fails_before_launching(backend):
     """A one-row MultiHeadAttention whose split partials exceed what the library's
     scratch holds cannot be captured: the call raises PUTER_ERR_INVALID inside the
