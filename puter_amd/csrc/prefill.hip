@@ -976,30 +976,33 @@ static bool launch_prefill_f32(const MhaArgs &m, hipStream_t s, int *status) {
     a.xcd_map = ((a.batch * a.kv_heads) % 8 == 0) ? 1 : 0;
     a.scale_log2 = m.scale * 1.4426950408889634f;
     const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;
-    // grids of fewer than 24 blocks stay on the general kernel (one block per query row
-    // and head): config 1's 128 queries x 8 heads of 64 (8 blocks) 14.2 against 15.8 us,
-    // 256 x 8 x 128 (16) 35.3 against 43.4; from 24 blocks this kernel wins (384 x 8 x
-    // 64: 32.9 against 36.0, 4 x 128 x 8 x 64: 15.0 against 24.5)
-    if (blocks < 24 || blocks > 0x7FFFFFFF) return false;
-    // small grids split each block's key range over blockIdx.y, partials in the
-    // library's scratch: the longest block's key loop, the critical path, shrinks with
-    // the split count.  Causal grids of under two blocks per CU aim at four blocks per
-    // CU in runs of at least 8 key tiles (the triangle leaves most CUs idle while the
-    // last query tiles run: B1 S4096 8 x 64 causal 296 -> 221 us, S2048 8 x 128 154 ->
-    // 146 us), other grids of under one block per CU at two, in runs of at least 16
-    // (B1 S2048 8 x 64, 150 -> 88 us; more splits lose there).  A stream that is
-    // capturing a graph keeps the unsplit kernel (the scratch cannot grow there)
+    if (blocks > 0x7FFFFFFF) return false;
     const int64_t cus = device_cus();
     const int64_t ktiles = (m.seq_k + 31) / 32;
+    hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(s, &cst) != hipSuccess || cst != hipStreamCaptureStatusNone;
+    // Grids of fewer than 24 blocks stay on the general kernel (one block per query
+    // row and head) unless they are causal over at least 8 key tiles and can split
+    // them (below): config 1's 128 queries x 8 heads of 64 (8 blocks) 9.2 us there
+    // against 14.2 here even split; 256 x 8 x 128 (16 blocks) 33.1 against 24.1 split
+    // (43 unsplit), 640 x 4 x 64 47.5 against 22.1.  From 24 blocks this kernel wins
+    // unsplit too (384 x 8 x 64: 32.9 against 36.0, 4 x 128 x 8 x 64: 15.0 against 24.5)
+    if (blocks < 24 && (!a.causal || ktiles < 8 || capturing)) return false;
+    // Small grids split each block's key range over blockIdx.y, partials in the
+    // library's scratch: the longest block's key loop, the critical path, shrinks with
+    // the split count.  Causal grids of under two blocks per CU aim at four blocks per
+    // CU in runs of at least 8 key tiles (2 under 24 blocks) (the triangle leaves most
+    // CUs idle while the last query tiles run: B1 S4096 8 x 64 causal 296 -> 221 us,
+    // S2048 8 x 128 154 -> 146 us), other grids of under one block per CU at two, in
+    // runs of at least 16 (B1 S2048 8 x 64, 150 -> 88 us; more splits lose there).  A
+    // stream that is capturing a graph keeps the unsplit kernel (the scratch cannot
+    // grow there)
     int64_t splits = 1;
     if (a.causal && blocks < 2 * cus)
-        splits = std::max<int64_t>(1, std::min<int64_t>((4 * cus + blocks - 1) / blocks, ktiles / 8));
+        splits = std::max<int64_t>(1, std::min<int64_t>((4 * cus + blocks - 1) / blocks, ktiles / (blocks < 24 ? 2 : 8)));
     else if (!a.causal && blocks < cus)
         splits = std::max<int64_t>(1, std::min<int64_t>((2 * cus + blocks - 1) / blocks, ktiles / 16));
-    if (splits > 1) {
-        hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(s, &cst) != hipSuccess || cst != hipStreamCaptureStatusNone) splits = 1;
-    }
+    if (capturing) splits = 1;
     if (splits > 1) {
         a.split_tiles = (int)((ktiles + splits - 1) / splits);
         splits = (ktiles + a.split_tiles - 1) / a.split_tiles;

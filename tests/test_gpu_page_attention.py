@@ -303,6 +303,8 @@ def test_mha(backend, dt, sq, sk, h, kvh, d, causal):
     (1024, 1024, 4, 1, 64, True),    # 32 blocks, 4 runs of 8 key tiles; the first query tile's last 3 are empty
     (200, 2100, 12, 4, 64, False),   # 24 blocks, 4 runs of 17 tiles, the last ragged
     (300, 1300, 8, 2, 128, True),    # head dim 128, causal shift 1000, 5 runs of 9 tiles, the last ragged
+    (256, 256, 8, 2, 128, True),     # 16 blocks (under 24: split in runs of 2 tiles, 4 runs)
+    (640, 640, 4, 4, 64, True),      # 20 blocks, 10 runs of 2 tiles
 ])
 def test_mha_f32_key_split(backend, sq, sk, h, kvh, d, causal):
     """f32 grids under one block per CU split each block's key range over blockIdx.y
