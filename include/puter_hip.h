@@ -22,7 +22,7 @@
  *     across blocks rather than inside them) and
  *     puter_hip_multi_head_attention[_batched] with seq_q == 1 (bf16 / f16 at
  *     head dim 128 without ALiBi, or any row over more than 768 keys) or in F32
- *     with at least 16 query rows, head dim 128 or 64, no window or ALiBi, and
+ *     with at least 16 query rows, head dim 128 or 64, and
  *     fewer 128-query blocks than two per CU (causal) or one per CU (not
  *     causal): one buffer per device, allocated on first use and grown on
  *     demand (Matmul: at most 16 MiB; one-row attention: the paged decode

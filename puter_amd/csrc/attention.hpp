@@ -24,7 +24,7 @@ struct MhaArgs {
 // MFMA flash prefill (prefill.hip).  Returns true and sets *status when the
 // shape is one it serves (bf16 / f16, head_dim 128 or 64, causal or not, sliding window, ALiBi;
 // head dim 64 only for more than one query row; f32, head_dim 128 or 64, at least 16
-// query rows, causal or not, no window or ALiBi).
+// query rows, causal or not, sliding window, ALiBi).
 bool launch_prefill_mfma(const MhaArgs &a, int dtype, hipStream_t s, int *status);
 // one query row per sequence (bf16 / f16, head_dim 128): the paged decode kernels
 bool launch_decode_contiguous(const MhaArgs &m, int dtype, hipStream_t s, int *status);

@@ -69,6 +69,8 @@
 // round-robin over the 8 XCDs), so the K/V tiles they re-read hit that XCD's L2.
 #include "attention.hpp"
 
+#include <climits>
+
 namespace puter {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -661,7 +663,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 // ------------------------------------------------------------ f32 prefill --
-// f32 MultiHeadAttention (head dim 128 or 64, causal or not, no window or ALiBi) on
+// f32 MultiHeadAttention (head dim 128 or 64, causal or not, sliding window, ALiBi) on
 // v_mfma_f32_32x32x2_f32: exact f32 products, f32 sums, softmax in f32 against a
 // running maximum (the reference's stableSoftmaxRow takes the row max, exp in
 // float64 and a sequential f32 sum; the order of the sums differs, the f32 bar
@@ -691,7 +693,7 @@ template <int D> struct PfF32Dim {
     static constexpr int vswz(int r) { return ((r >> 2) & 1) << 3; }   // in chunks (8 = 32 floats)
 };
 
-template <int D>
+template <int D, bool GEN>
 __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
     using T = PfF32Dim<D>;
     constexpr int BM = fa::BM, BN = T::BN;
@@ -749,6 +751,15 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
     int nfree = a.seq_k / BN;
     if (a.causal) nfree = min(nfree, q0 + a.shift + 1 > 0 ? (q0 + a.shift + 1) / BN : 0);
     nfree = min(nfree, ntiles);
+    if (GEN && a.alibi_s != 0.0f) nfree = 0;   // the bias is added by the masked step only
+    // a sliding window: the tiles below the block's first query's window are skipped,
+    // those below its last query's window edge masked ([wlo, wfree))
+    int wlo = 0, wfree = 0;
+    if (GEN && a.window > 0) {
+        const int qmax = min(q0 + BM, a.seq_q) - 1;
+        wlo = min(max(0, q0 - a.window + 1) / BN, ntiles);
+        wfree = max(wlo, (max(0, qmax - a.window + 1) + BN - 1) / BN);
+    }
 
     // copy offsets (source side, swizzled): wave w fills rows 4 RPI i + RPI w + lane / NC
     int kg[4], vg[4];
@@ -807,13 +818,23 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
             for (int s4 = 0; s4 < 4; ++s4) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[s4], qf[g][s4], sacc, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);   // one group's K read live at a time
         }
-        // register r: key kv0 + 8 (r / 4) + 4 h + r % 4, query qi
+        // register r: key kv0 + 8 (r / 4) + 4 h + r % 4, query qi.  The masked step
+        // also adds ALiBi's alibi_s * (k - q) (before the scale: slope * (k - q) on the
+        // scaled score, typed_compute.go:176-178) and hides keys below the window
         if (masked) {
             const int last = a.causal ? min(qi + a.shift, a.seq_k - 1) : a.seq_k - 1;
             const int lim = last - kv0 - 4 * h;
+            const int lo = GEN && a.window > 0 ? qi - a.window + 1 - kv0 - 4 * h : INT_MIN;
+            if (GEN && a.alibi_s != 0.0f) {
+                const float base = (float)(kv0 + 4 * h - qi);
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (8 * (r >> 2) + (r & 3) > lim) sacc[r] = -INFINITY;
+                for (int r = 0; r < 16; ++r) sacc[r] += a.alibi_s * (base + (float)(8 * (r >> 2) + (r & 3)));
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 8 * (r >> 2) + (r & 3);
+                if (off > lim || off < lo) sacc[r] = -INFINITY;
+            }
         }
         float tmax = -INFINITY;
 #pragma unroll
@@ -855,11 +876,13 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
         }
     };
 
-    // this block's key tiles: all, or split blockIdx.y's run of split_tiles
-    int tlo = 0, thi = ntiles;
+    // this block's key tiles: from the window's lower edge on, all of them or split
+    // blockIdx.y's run of split_tiles
+    int tlo = wlo, thi = ntiles;
     if (a.split_tiles > 0) {
-        tlo = min(ntiles, (int)blockIdx.y * a.split_tiles);
-        thi = min(ntiles, tlo + a.split_tiles);
+        const int ylo = min(ntiles, (int)blockIdx.y * a.split_tiles);
+        tlo = max(tlo, ylo);
+        thi = min(ntiles, ylo + a.split_tiles);
     }
     if (tlo < thi) copy_tile(tlo * BN, k0s, v0s);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
@@ -867,8 +890,11 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(PrefillArgs a) {
     auto tile = [&](int it, const char *kc, const char *vc, char *kn, char *vn) __attribute__((always_inline)) {
         const int kv0 = it * BN;
         if (it + 1 < thi) copy_tile(kv0 + BN, kn, vn);
-        if (it < nfree) step(kc, vc, kv0, false);
-        else if (!a.causal || kv0 <= qlast + a.shift) step(kc, vc, kv0, true);   // waves whose queries all precede it skip it
+        // waves whose queries all precede the tile, or whose windows all start past it,
+        // skip it
+        const bool seen = (!a.causal || kv0 <= qlast + a.shift) && (!GEN || a.window <= 0 || kv0 + BN - 1 >= qfirst - a.window + 1);
+        if (it >= wfree && it < nfree) step(kc, vc, kv0, false);
+        else if (seen) step(kc, vc, kv0, true);
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
     };
@@ -948,10 +974,10 @@ __global__ __launch_bounds__(256) void prefill_f32_combine_kernel(PrefillArgs a,
 }
 
 // f32 MultiHeadAttention on prefill_f32_kernel: head dim 128 or 64, at least 16 query
-// rows, no sliding window or ALiBi (those keep the general kernel).
+// rows, causal or not, with or without a sliding window and ALiBi.
 static bool launch_prefill_f32(const MhaArgs &m, hipStream_t s, int *status) {
     if (m.dim != 128 && m.dim != 64) return false;
-    if (m.seq_q < 16 || m.alibi != 0.0f || (m.window > 0 && m.window < m.seq_q)) return false;
+    if (m.seq_q < 16) return false;
     if (m.seq_q > 0x3FFFFFFF || m.seq_k > 0x3FFFFFFF || m.shift > 0x3FFFFFFF || m.shift < -0x3FFFFFFF) return false;
     if (m.kv_heads > 32768) return false;   // a 32-row K/V tile spans < 2^31 bytes
     const uintptr_t mask = 15;
@@ -971,10 +997,13 @@ static bool launch_prefill_f32(const MhaArgs &m, hipStream_t s, int *status) {
     a.qtiles = (int)((m.seq_q + fa::BM - 1) / fa::BM);
     a.causal = m.causal;
     a.shift = (int)m.shift;
-    a.window = 0;
-    a.alibi_s = 0.0f;
+    // a window of seq_q or more hides no key (a query's distance to a visible key is
+    // below seq_q): run it as no window
+    a.window = (m.window > 0 && m.window < m.seq_q) ? (int)m.window : 0;
+    a.alibi_s = m.alibi != 0.0f ? m.alibi / m.scale : 0.0f;
     a.xcd_map = ((a.batch * a.kv_heads) % 8 == 0) ? 1 : 0;
     a.scale_log2 = m.scale * 1.4426950408889634f;
+    const bool gen = a.window > 0 || a.alibi_s != 0.0f;   // the kernel with the window / ALiBi code
     const int64_t blocks = (int64_t)a.qtiles * a.batch * a.heads;
     if (blocks > 0x7FFFFFFF) return false;
     const int64_t cus = device_cus();
@@ -1019,10 +1048,12 @@ static bool launch_prefill_f32(const MhaArgs &m, hipStream_t s, int *status) {
         const dim3 grid((unsigned)blocks, (unsigned)splits);
         const unsigned cblocks = (unsigned)((rows + 3) / 4);
         if (m.dim == 128) {
-            prefill_f32_kernel<128><<<grid, 256, 0, s>>>(a);
+            if (gen) prefill_f32_kernel<128, true><<<grid, 256, 0, s>>>(a);
+            else prefill_f32_kernel<128, false><<<grid, 256, 0, s>>>(a);
             prefill_f32_combine_kernel<128><<<cblocks, 256, 0, s>>>(a, (int)splits, rows);
         } else {
-            prefill_f32_kernel<64><<<grid, 256, 0, s>>>(a);
+            if (gen) prefill_f32_kernel<64, true><<<grid, 256, 0, s>>>(a);
+            else prefill_f32_kernel<64, false><<<grid, 256, 0, s>>>(a);
             prefill_f32_combine_kernel<64><<<cblocks, 256, 0, s>>>(a, (int)splits, rows);
         }
         const int rc = check_launch("prefill f32 mfma split");
@@ -1030,8 +1061,13 @@ static bool launch_prefill_f32(const MhaArgs &m, hipStream_t s, int *status) {
         *status = rc ? rc : fin;
         return true;
     }
-    if (m.dim == 128) prefill_f32_kernel<128><<<(unsigned)blocks, 256, 0, s>>>(a);
-    else prefill_f32_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(a);
+    if (m.dim == 128) {
+        if (gen) prefill_f32_kernel<128, true><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else prefill_f32_kernel<128, false><<<(unsigned)blocks, 256, 0, s>>>(a);
+    } else {
+        if (gen) prefill_f32_kernel<64, true><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else prefill_f32_kernel<64, false><<<(unsigned)blocks, 256, 0, s>>>(a);
+    }
     *status = check_launch("prefill f32 mfma");
     return true;
 }

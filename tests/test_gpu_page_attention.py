@@ -492,21 +492,23 @@ def test_prefill_mfma_shapes(backend, dt, d, b, sq, sk, h, kvh, causal):
     (1, 300, 77, 8, 8, False, 50),      # non-causal: queries past key 76 + 50 see no key
     (1, 700, 700, 4, 2, False, 300),    # non-causal, edge crosses several tiles per block
 ])
-@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
 @pytest.mark.parametrize("d", [128, 64])
 def test_prefill_mfma_window(backend, dt, d, b, sq, sk, h, kvh, causal, window):
-    """Sliding-window prefill on the MFMA kernel (query q sees key k only if
+    """Sliding-window prefill on the MFMA kernels (query q sees key k only if
     q - k < window, typed_compute.go:172) against the oracle; rows with no
-    visible key are exactly zero."""
+    visible key are exactly zero.  f32 runs on the f32 MFMA kernel where the grid
+    takes it (at least 24 blocks, or causal over at least 8 key tiles) and on the
+    general kernel otherwise."""
     import puter_amd
     std = 1.0 / np.sqrt(d)
     q = encode(seeded(310 + sq, (b, sq, h * d), 0.0, std), dt)
     k = encode(seeded(311 + sk, (b, sk, kvh * d), 0.0, std), dt)
     v = encode(seeded(312 + sk, (b, sk, kvh * d)), dt)
-    out = empty_dev((b, sq, h * d), np.uint16)
+    out = empty_dev((b, sq, h * d), NP[dt])
     cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, window, 0.0, kvh)
     backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, sq, sk, dt)
-    got = decode(to_host(out, np.uint16), dt)
+    got = decode(to_host(out, NP[dt]), dt)
     O.set_threads(8)
     shift = sk - sq
     for i in range(b):
@@ -524,20 +526,20 @@ def test_prefill_mfma_window(backend, dt, d, b, sq, sk, h, kvh, causal, window):
     (1, 200, 520, 4, 2, True, 100, 0.5),     # seqK > seqQ with a window and ALiBi
     (1, 96, 40, 4, 4, True, 0, -0.125),      # negative slope; leading queries see no key
 ])
-@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
 @pytest.mark.parametrize("d", [128, 64])
 def test_prefill_mfma_alibi(backend, dt, d, b, sq, sk, h, kvh, causal, window, alibi):
-    """ALiBi prefill on the MFMA kernel (score += slope * (k - q) on the scaled
+    """ALiBi prefill on the MFMA kernels (score += slope * (k - q) on the scaled
     score, typed_compute.go:176-178; with or without a window) against the oracle."""
     import puter_amd
     std = 1.0 / np.sqrt(d)
     q = encode(seeded(330 + sq, (b, sq, h * d), 0.0, std), dt)
     k = encode(seeded(331 + sk, (b, sk, kvh * d), 0.0, std), dt)
     v = encode(seeded(332 + sk, (b, sk, kvh * d)), dt)
-    out = empty_dev((b, sq, h * d), np.uint16)
+    out = empty_dev((b, sq, h * d), NP[dt])
     cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, window, alibi, kvh)
     backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, sq, sk, dt)
-    got = decode(to_host(out, np.uint16), dt)
+    got = decode(to_host(out, NP[dt]), dt)
     O.set_threads(8)
     for i in range(b):
         ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, window=window, alibi=alibi,
