@@ -321,6 +321,48 @@ def test_mha_f32_key_split(backend, sq, sk, h, kvh, d, causal):
     assert_close(decode(to_host(out, NP[dt]), dt), ref, TOL[dt], elem_tol=1e-3, what="mha split")
 
 
+def _random_mha_cases(n, seed):
+    """Seeded random MultiHeadAttention shapes across the routing rules: grid sizes
+    on both sides of the f32 kernel's 24-block and split thresholds, ragged tiles,
+    seqK above and below seqQ, GQA groups, windows and ALiBi slopes."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        d = int(rng.choice([64, 128]))
+        kvh = int(rng.choice([1, 2, 4]))
+        h = kvh * int(rng.choice([1, 2, 4]))
+        sq = int(rng.integers(16, 700))
+        sk = int(max(1, sq + rng.integers(-sq // 2, 600)))
+        b = int(rng.choice([1, 2]))
+        causal = bool(rng.integers(0, 2))
+        window = int(rng.choice([0, 0, int(rng.integers(1, 300))]))
+        alibi = float(rng.choice([0.0, 0.0, 0.0625, -0.125]))
+        cases.append((b, sq, sk, h, kvh, d, causal, window, alibi))
+    return cases
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("case", _random_mha_cases(10, 4242))
+def test_mha_random_shapes(backend, dt, case):
+    """MultiHeadAttentionBatched on seeded random shapes against the oracle, each
+    batch element separately (the reference's per-call layout)."""
+    import puter_amd
+    b, sq, sk, h, kvh, d, causal, window, alibi = case
+    std = 1.0 / np.sqrt(d)
+    q = encode(seeded(400 + sq, (b, sq, h * d), 0.0, std), dt)
+    k = encode(seeded(401 + sk, (b, sk, kvh * d), 0.0, std), dt)
+    v = encode(seeded(402 + sk, (b, sk, kvh * d)), dt)
+    out = empty_dev((b, sq, h * d), NP[dt])
+    cfg = puter_amd.MultiHeadAttentionConfig(h, d, causal, window, alibi, kvh)
+    backend.MultiHeadAttentionBatched(cfg, to_dev(q), to_dev(k), to_dev(v), out, b, sq, sk, dt)
+    got = decode(to_host(out, NP[dt]), dt)
+    O.set_threads(8)
+    for i in range(b):
+        ref = decode(O.mha(q[i], k[i], v[i], h, d, causal=causal, kv_heads=kvh, window=window, alibi=alibi,
+                           dtype=dt), dt)
+        assert_close(got[i], ref, TOL[dt], elem_tol=None, what=f"random mha {case} batch {i}")
+
+
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("b,sk,h,kvh,causal,window", [
     (1, 4096, 32, 8, True, 0),     # configs[4]'s heads at one sequence's full context
