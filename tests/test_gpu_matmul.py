@@ -80,6 +80,46 @@ def test_matmul_16bit_exact_integer_products(backend, dt, rows, inner, cols):
     assert bad.size == 0, f"{bad.shape[0]} cells differ, e.g. {bad[:4].tolist()}: {got[tuple(bad[:4].T)]} vs {want[tuple(bad[:4].T)]}"
 
 
+def _random_matmul_shapes(n, seed):
+    """Seeded random shapes across the Matmul routing rules: the small in-block
+    split-K kernels, the 16-bit skinny split-K kernel (few rows or few tiles), the f32
+    MFMA kernel split or not, the 128 x 128 and 256 x 256 16-bit tiles, and K / N
+    that are not multiples of 4 or 8 (the generic kernels)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        rows = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 600)), int(rng.integers(600, 2500))]))
+        inner = int(rng.choice([int(rng.integers(1, 128)), int(rng.integers(128, 1200)), int(rng.integers(1200, 4200))]))
+        cols = int(rng.choice([int(rng.integers(1, 256)), int(rng.integers(256, 2600))]))
+        if rng.integers(0, 2):   # aligned half the time
+            inner, cols = max(8, inner // 8 * 8), max(8, cols // 8 * 8)
+        out.append((rows, inner, cols))
+    return out
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+@pytest.mark.parametrize("rows,inner,cols", _random_matmul_shapes(12, 777))
+def test_matmul_random_exact_integer_products(backend, dt, rows, inner, cols):
+    """Small integer operands keep every partial sum exact in f32 whatever the kernel,
+    tiling or split, so every output equals the exact product narrowed once to the
+    output format, bit for bit; NaN-poisoned output catches a missing or misplaced
+    element."""
+    rng = np.random.default_rng(rows + 7 * inner + 3 * cols + dt)
+    ai = rng.integers(-3, 4, (rows, inner)).astype(np.float32)
+    bi = rng.integers(-2, 3, (inner, cols)).astype(np.float32)
+    exact = (ai.astype(np.float64) @ bi.astype(np.float64)).astype(np.float32)
+    if dt == O.F32:
+        a, b, want, npt = ai, bi, exact, np.float32
+    else:
+        a, b, want, npt = O.from_f32(ai, dt), O.from_f32(bi, dt), O.from_f32(exact, dt), np.uint16
+    out = empty_dev((rows, cols), npt)
+    out.fill_(float("nan") if npt == np.float32 else 0x7FC0)
+    backend.Matmul(out, to_dev(a), to_dev(b), rows, inner, cols, dt)
+    got = to_host(out, npt)
+    bad = np.argwhere(got.view(np.uint8).reshape(rows, -1) != want.view(np.uint8).reshape(rows, -1))
+    assert bad.size == 0, f"{bad.shape[0]} bytes differ at {rows}x{inner}x{cols}, e.g. {bad[:4].tolist()}"
+
+
 @pytest.mark.parametrize("rows,inner,cols", [(4000, 264, 4104), (2048, 100, 2052), (2100, 64, 2048)])
 def test_matmul_f32_exact_integer_products(backend, rows, inner, cols):
     """F32 outputs of at least 256 tiles of 128 x 128 take the f32 MFMA kernel: small
