@@ -791,11 +791,12 @@ def test_paged_decode_bad_page_ids_are_masked(backend, kv_dt):
 
 
 @pytest.mark.parametrize("kv_dt", [O.BF16, O.F8E4M3])
-@pytest.mark.parametrize("batch,lo,hi", [(70, 1, 600), (300, 1, 40)])
+@pytest.mark.parametrize("batch,lo,hi", [(70, 1, 600), (256, 1, 40), (300, 1, 40)])
 def test_paged_decode_empty_sequences_and_batches(backend, kv_dt, batch, lo, hi):
     """Sequences of zero context among live ones in batches of 70 (fp8 pools number
     the live (sequence, split) pairs with a prefix sum over 64 sequences at a time:
-    two passes) and 300 (past 256 sequences the plain block order).  A sequence with
+    two passes), 256 (four passes, the largest batch numbered so) and 300 (past 256
+    sequences the plain block order).  A sequence with
     no key has no reference output (the reference's gather yields no rows and its
     zero-size attention call returns early); this extension writes zeros for it.  The
     live sequences match the oracle run on them alone."""
